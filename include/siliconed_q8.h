@@ -1,0 +1,161 @@
+/*
+ * siliconed_q8.h — C ABI of the MI355X (gfx950) weight-quantized linear layer.
+ *
+ * The drop-in boundary for Siliconed's weight-product path: the Swift host keeps its operator API
+ * (`WeightProducts.linear`, Sources/Siliconed/WeightProducts.swift:278, and its planning) and calls
+ * these entry points where it encoded Metal work through `TensorGEMM`
+ * (Sources/Siliconed/TensorGEMM.swift:206-360, TensorGEMMBF16.swift:208-264). Plain pointers and
+ * sizes only; every pointer to tensor data is a device pointer the caller allocated and owns.
+ *
+ * Arithmetic (the reference's, TensorGEMM.swift:124-135 then :173-179): C = act(s ⊙ (A · q) + b)
+ * with q the 8-bit codes widened exactly, fp32 sums, the scale applied after the sum, the bias
+ * added after the scale (Ops.swift:400-407), the activation last.
+ *
+ * Status codes: 0 = success; > 0 = the call was refused before any work (invalid argument or a
+ * configuration this library does not run: the caller keeps its widened route, as it does when
+ * `TensorGEMM.init?` returns nil); < 0 = a HIP error, negated. No entry point aborts.
+ *
+ * Threading: a context is used by one host thread at a time (no internal locks); contexts on
+ * different streams may run concurrently (Sources/Siliconed/Engine.swift:19 runs one render at a
+ * time; GEMM.swift:166-194 guards only counters).
+ */
+#ifndef SILICONED_Q8_H
+#define SILICONED_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SQ8_ABI_VERSION 1
+
+/* ---- status ---- */
+enum sq8_status {
+    SQ8_OK = 0,
+    SQ8_EINVAL = 1,        /* a null pointer, a negative size, a stride shorter than a row */
+    SQ8_EUNSUPPORTED = 2,  /* a valid configuration this library does not run */
+    SQ8_ENODEVICE = 3,     /* no gfx950 device at that ordinal */
+};
+
+/* ---- element types (Artifact.DType, Sources/Siliconed/Artifact.swift:65-113) ---- */
+enum sq8_dtype {
+    SQ8_BF16 = 1,
+    SQ8_F32 = 2,
+    SQ8_INT8 = 3,
+    SQ8_FP8_E4M3 = 4,      /* "fn": bias 7, no infinity, 0x7F/0xFF NaN (Forge/Numerics.swift:48-55) */
+    SQ8_F16 = 5,
+};
+
+/* ---- weight layouts ---- */
+enum sq8_wlayout {
+    SQ8_KN = 0,            /* [K, N] row-major, N contiguous: the map's layout
+                              (`linear_weights_transposed`, Artifact.swift:655) */
+    SQ8_NK = 1,            /* [N, K] row-major, K contiguous: a published nn.Linear */
+};
+
+/* ---- scale layouts (Widen.ScaleLayout, Sources/Siliconed/Widen.swift:100-110) ---- */
+enum sq8_scale_layout {
+    SQ8_SCALE_TENSOR = 0,  /* one scale: `perColumn` false (TensorGEMM.swift:264, :353) */
+    SQ8_SCALE_COLUMNS = 1, /* one per output channel: `perColumn` true */
+    SQ8_SCALE_BLOCKS = 2,  /* [K/b, N] (dequantize only) */
+    SQ8_SCALE_ROWS = 3,    /* one per row of [N, K] (dequantize only) */
+};
+
+/* ---- epilogues ---- */
+enum sq8_epilogue {
+    SQ8_EPI_NONE = 0,      /* C = s ⊙ (A·q) (+ b) */
+    SQ8_EPI_GELU_TANH = 1, /* nn.GELU(approximate="tanh") (Ops.swift:386-398) */
+    SQ8_EPI_SILU_GLU = 2,  /* n = 2h, output h: silu(gate)·up, gate = columns [0, h)
+                              (ElementwiseGPU.swift:67-73 on Block.swift:499-504's w1/w3) */
+    SQ8_EPI_SITU_GLU = 3,  /* n = 2h, output h: 4·tanh(g/4)·σ(g)·25·tanh(v/25), value = columns
+                              [0, h), gate = [h, 2h) (MossImage.swift:874-876, 889-900) */
+};
+
+typedef struct sq8_ctx sq8_ctx;
+
+/* Creates a context on HIP device `device`, launching on `stream` (a hipStream_t; NULL = the
+ * device's null stream). Refuses (SQ8_ENODEVICE) a device that is not gfx950.
+ * Replaces: TensorGEMM.init?(device:queue:roundingActivations:quantizingActivations:)
+ * (Sources/Siliconed/TensorGEMM.swift:206-232). */
+int sq8_create(int device, void *stream, sq8_ctx **out);
+
+/* Releases the context and its scratch memory. Replaces: the TensorGEMM instance's release. */
+int sq8_destroy(sq8_ctx *ctx);
+
+/* Changes the stream later launches go to. Replaces: the command queue passed at init
+ * (TensorGEMM.swift:206). */
+int sq8_set_stream(sq8_ctx *ctx, void *stream);
+
+/* 0 when `sq8_linear` runs this combination, else SQ8_EUNSUPPORTED / SQ8_EINVAL — the caller then
+ * keeps the widened route. Replaces: the nil checks on `TensorGEMM.rounded`/`.int8`
+ * (TensorGEMM.swift:218-229, `roundsActivations`, `readsBlocks`). */
+int sq8_supports(const sq8_ctx *ctx, int a_dtype, int w_dtype, int w_layout, int scale_layout,
+                 int c_dtype, int epilogue);
+
+/* **The product**: C[m, n_out] = act(s ⊙ (A[m, k] · W) + b), W the 8-bit codes of `w_dtype` in
+ * `w_layout` with leading dimension `ldw` (elements), `scale` fp32 ([n] per column or [1] per
+ * tensor), `bias` fp32 [n] or NULL, A of `a_dtype` (SQ8_BF16, or SQ8_F32: rounded to bf16
+ * nearest-even first, as `submitRounded` rounds its operand, TensorGEMMBF16.swift:41-48, 208-264),
+ * C of `c_dtype` (SQ8_F32 as the reference writes it, or SQ8_BF16), written, not accumulated.
+ * n_out = n, or n/2 for the GLU epilogues. A computes only the first `n` columns of a wider W when
+ * `ldw`/`ldc` say so (the `columns` argument of `submit`, TensorGEMM.swift:296).
+ * `gpu_seconds`: NULL → the launch is queued and the call returns at once (`settled`,
+ * TensorGEMM.swift:261-263); non-NULL → the call waits and writes the kernel's GPU seconds
+ * (TensorGEMM.swift:268-272, `Attention.verdict`).
+ * Replaces: TensorGEMM.linear(a:int8:weightOffset:scales:scalesOffset:perColumn:block:rotation:
+ * rounding:quantizing:prequantized:c:m:k:n:settled:) -> Double (TensorGEMM.swift:264-290) and
+ * its encoders submit (:296-360) / submitRounded (TensorGEMMBF16.swift:208-264), with the bias
+ * (DiT.swift:403-413) and activation passes (Ops.swift:386-398, ElementwiseGPU.swift:67-73,
+ * MossImage.swift:889-900) fused. */
+int sq8_linear(sq8_ctx *ctx,
+               const void *a, int a_dtype, int64_t lda,
+               const void *w, int w_dtype, int w_layout, int64_t ldw,
+               const float *scale, int scale_layout,
+               const float *bias, int epilogue,
+               void *c, int c_dtype, int64_t ldc,
+               int m, int k, int n, double *gpu_seconds);
+
+/* **The fused QKV product**: one product of n = 3·d columns whose output columns [0,d), [d,2d),
+ * [2d,3d) go to `q`, `k`, `v`. `head_dim` = 0: each output is [m, d] row-major (leading
+ * dimension `ldo`); `head_dim` > 0: each is [d/head_dim, m, head_dim] (heads outermost, the layout
+ * an attention kernel reads), `ldo` ignored. Epilogue: none (bias added if given).
+ * Replaces: the MOSS text block's fused qkv product, bias pass and row split
+ * (MossImage.swift:548-560); the DiT blocks' three products on one operand (Block.swift:410-415). */
+int sq8_linear_qkv(sq8_ctx *ctx,
+                   const void *a, int a_dtype, int64_t lda,
+                   const void *w, int w_dtype, int w_layout, int64_t ldw,
+                   const float *scale, int scale_layout, const float *bias,
+                   void *q, void *k_out, void *v, int c_dtype, int64_t ldo, int head_dim,
+                   int m, int k, int d, double *gpu_seconds);
+
+/* **The dequantiser on the device**: out[i] = Float(code[i]) · s[layout(i)], one fp32 multiply
+ * (never fused), for `rows` × `columns` codes in row-major order; scale fp32/bf16/fp16
+ * (`scale_dtype`), NULL → the plain conversion. `block_rows`: rows per scale (BLOCKS);
+ * `first_row`: the row of codes[0] in the whole tensor (BLOCKS, ROWS). The codes go through the
+ * same conversion the product uses, so this is the bit-exact check of it.
+ * Replaces: Widen.dequantize (Sources/Siliconed/Widen.swift:129-271) as reached from
+ * Artifact.materialize (Artifact.swift:670-713). */
+int sq8_dequantize(sq8_ctx *ctx, const void *codes, int w_dtype, int64_t rows, int64_t columns,
+                   const void *scale, int scale_dtype, int scale_layout, int64_t block_rows,
+                   int64_t first_row, float *out);
+
+/* fp32 → bf16, nearest-even, NaN kept quiet (2·count bytes written).
+ * Replaces: the `round_bf16` pass (TensorGEMMBF16.swift:41-48, 67-73). */
+int sq8_round_bf16(sq8_ctx *ctx, const float *x, uint16_t *y, int64_t count);
+
+/* Waits for everything queued on the context's stream. Replaces: waitUntilCompleted /
+ * GPUStream.drain (GPUStream.swift). */
+int sq8_synchronize(sq8_ctx *ctx);
+
+/* A static English string for a status code (never NULL). */
+const char *sq8_status_string(int status);
+
+/* SQ8_ABI_VERSION of the library. */
+int sq8_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,369 @@
+/*
+ * sq8_oracle.c — CPU restatement of the reference's arithmetic for the weight-quantized linear
+ * layer. TEST INFRASTRUCTURE ONLY (see sq8_oracle.h). Built with -ffp-contract=off: every product
+ * below rounds once, as the reference's vDSP passes do (Sources/Siliconed/Widen.swift:94-97).
+ */
+#include "sq8_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+int orc_version(void) { return 1; }
+
+/* ---------------------------------------------------------------------------------------------
+ * SplitMix64 and Box–Muller: Sources/Verification/KernelStages.swift:553-567.
+ * uniform = (z >> 11) / 2^53; normal = sqrt(−2·log(max(u1, 1e−300)))·cos(2π·u2).
+ * ------------------------------------------------------------------------------------------- */
+uint64_t orc_splitmix_next(uint64_t *state) {
+    *state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+double orc_splitmix_uniform(uint64_t *state) {
+    return (double)(orc_splitmix_next(state) >> 11) / 9007199254740992.0; /* 2^53 */
+}
+
+double orc_splitmix_normal(uint64_t *state) {
+    double u1 = orc_splitmix_uniform(state);
+    double u2 = orc_splitmix_uniform(state);
+    return sqrt(-2.0 * log(u1 > 1e-300 ? u1 : 1e-300)) * cos(2.0 * M_PI * u2);
+}
+
+/* Draw i of a stream depends on i only through the state after 2·i steps, so a long fill is
+ * cut into chunks whose states are computed directly (state after j steps = seed + j·γ). */
+#define ORC_CHUNK ((size_t)1 << 16)
+
+void orc_fill_normal_f32(uint64_t seed, double mean, double std, float *out, size_t count) {
+    long chunks = (long)((count + ORC_CHUNK - 1) / ORC_CHUNK);
+#pragma omp parallel for schedule(static)
+    for (long c = 0; c < chunks; ++c) {
+        size_t first = (size_t)c * ORC_CHUNK, end = first + ORC_CHUNK < count ? first + ORC_CHUNK : count;
+        uint64_t state = seed + (uint64_t)(2 * first) * 0x9E3779B97F4A7C15ull;
+        for (size_t i = first; i < end; ++i) out[i] = (float)(mean + std * orc_splitmix_normal(&state));
+    }
+}
+
+void orc_fill_normal_bf16(uint64_t seed, double mean, double std, uint16_t *out, size_t count) {
+    long chunks = (long)((count + ORC_CHUNK - 1) / ORC_CHUNK);
+#pragma omp parallel for schedule(static)
+    for (long c = 0; c < chunks; ++c) {
+        size_t first = (size_t)c * ORC_CHUNK, end = first + ORC_CHUNK < count ? first + ORC_CHUNK : count;
+        uint64_t state = seed + (uint64_t)(2 * first) * 0x9E3779B97F4A7C15ull;
+        for (size_t i = first; i < end; ++i)
+            out[i] = orc_f32_to_bf16((float)(mean + std * orc_splitmix_normal(&state)));
+    }
+}
+
+void orc_fill_uniform_f32(uint64_t seed, double lo, double hi, float *out, size_t count) {
+    long chunks = (long)((count + ORC_CHUNK - 1) / ORC_CHUNK);
+#pragma omp parallel for schedule(static)
+    for (long c = 0; c < chunks; ++c) {
+        size_t first = (size_t)c * ORC_CHUNK, end = first + ORC_CHUNK < count ? first + ORC_CHUNK : count;
+        uint64_t state = seed + (uint64_t)first * 0x9E3779B97F4A7C15ull;
+        for (size_t i = first; i < end; ++i) out[i] = (float)(lo + (hi - lo) * orc_splitmix_uniform(&state));
+    }
+}
+
+void orc_fill_uniform_i8(uint64_t seed, int lo, int hi, int8_t *out, size_t count) {
+    long chunks = (long)((count + ORC_CHUNK - 1) / ORC_CHUNK);
+    double span = (double)(hi - lo + 1);
+#pragma omp parallel for schedule(static)
+    for (long c = 0; c < chunks; ++c) {
+        size_t first = (size_t)c * ORC_CHUNK, end = first + ORC_CHUNK < count ? first + ORC_CHUNK : count;
+        uint64_t state = seed + (uint64_t)first * 0x9E3779B97F4A7C15ull;
+        for (size_t i = first; i < end; ++i) {
+            int v = lo + (int)floor(orc_splitmix_uniform(&state) * span);
+            out[i] = (int8_t)(v > hi ? hi : v);
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Conversions.
+ * ------------------------------------------------------------------------------------------- */
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* Sources/Siliconed/TensorGEMMBF16.swift:43-47: a NaN stays a quiet NaN (sign and payload kept,
+ * quiet bit set), else add 0x7FFF plus the lowest kept bit and shift — an overflow rounds to ∞. */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u = f32_bits(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+/* Sources/Siliconed/Widen.swift:25-49: the sixteen bits at the head of a 32-bit word. */
+float orc_bf16_to_f32(uint16_t b) { return bits_f32((uint32_t)b << 16); }
+
+/* Sources/Siliconed/Forge/Numerics.swift:48-55: sign, e = bits 6..3, m = bits 2..0, bias 7;
+ * e = 15 and m = 7 is NaN; e = 0 is m/8·2^−6; else (1 + m/8)·2^(e−7). No infinity. */
+float orc_e4m3_to_f32(uint8_t b) {
+    float sign = (b & 0x80) ? -1.0f : 1.0f;
+    int e = (b >> 3) & 0xF, m = b & 0x7;
+    if (e == 0xF && m == 0x7) return NAN;
+    if (e == 0) return sign * (float)m / 8.0f * ldexpf(1.0f, -6);
+    return sign * (1.0f + (float)m / 8.0f) * ldexpf(1.0f, e - 7);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    int e = (h >> 10) & 0x1F;
+    uint32_t m = h & 0x3FFu;
+    if (e == 0x1F) return bits_f32(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        float v = (float)m * ldexpf(1.0f, -24);
+        return sign ? -v : v;
+    }
+    return bits_f32(sign | ((uint32_t)(e - 15 + 127) << 23) | (m << 13));
+}
+
+uint8_t orc_f32_to_e4m3(float f) {
+    if (isnan(f)) return 0x7F;
+    uint8_t sign = signbit(f) ? 0x80 : 0x00;
+    double a = fabs((double)f);
+    if (a >= 448.0) return sign | 0x7E;
+    uint8_t code;
+    if (a < 0.015625) {                                   /* below 2^−6: subnormal step 2^−9 */
+        double q = nearbyint(a * 512.0);                  /* ties to even */
+        code = (uint8_t)q;                                /* q == 8 is 2^−6, code 0x08 */
+    } else {
+        int e;
+        double frac = frexp(a, &e);                       /* a = frac·2^e, frac in [0.5, 1) */
+        e -= 1;                                           /* a = (2·frac)·2^e, 2·frac in [1, 2) */
+        double q = nearbyint((2.0 * frac - 1.0) * 8.0);
+        if (q == 8.0) { q = 0.0; e += 1; }
+        int field = e + 7;
+        code = (uint8_t)((field << 3) | (int)q);
+        if (code > 0x7E) code = 0x7E;
+    }
+    return sign | code;
+}
+
+void orc_quantize_e4m3(const float *x, uint8_t *out, size_t count) {
+    long n = (long)count;
+#pragma omp parallel for schedule(static) if (n > (1L << 16))
+    for (long i = 0; i < n; ++i) out[i] = orc_f32_to_e4m3(x[i]);
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Dequantiser: Sources/Siliconed/Widen.swift:129-271.
+ * ------------------------------------------------------------------------------------------- */
+static inline float code_value(const void *values, int kind, size_t i) {
+    if (kind == ORC_INT8) return (float)((const int8_t *)values)[i];
+    return orc_e4m3_to_f32(((const uint8_t *)values)[i]);
+}
+
+static inline float scale_value(const void *scale, int scale_type, size_t i) {
+    switch (scale_type) {
+    case ORC_BF16: return orc_bf16_to_f32(((const uint16_t *)scale)[i]);
+    case ORC_F16: return orc_f16_to_f32(((const uint16_t *)scale)[i]);
+    default: return ((const float *)scale)[i];
+    }
+}
+
+void orc_dequantize(const void *values, int kind, size_t count, const void *scale, int scale_type,
+                    int layout, size_t columns, size_t block_rows, size_t first_row, float *out) {
+    long n = (long)count;
+    if (!scale) {
+#pragma omp parallel for schedule(static) if (n > (1L << 17))
+        for (long i = 0; i < n; ++i) out[i] = code_value(values, kind, (size_t)i);
+        return;
+    }
+    switch (layout) {
+    case ORC_SCALE_TENSOR: {
+        float s = scale_value(scale, scale_type, 0);
+#pragma omp parallel for schedule(static) if (n > (1L << 17))
+        for (long i = 0; i < n; ++i) out[i] = code_value(values, kind, (size_t)i) * s;
+        break;
+    }
+    case ORC_SCALE_COLUMNS:
+#pragma omp parallel for schedule(static) if (n > (1L << 17))
+        for (long i = 0; i < n; ++i)
+            out[i] = code_value(values, kind, (size_t)i) * scale_value(scale, scale_type, (size_t)i % columns);
+        break;
+    case ORC_SCALE_BLOCKS:
+#pragma omp parallel for schedule(static) if (n > (1L << 17))
+        for (long i = 0; i < n; ++i) {
+            size_t row = first_row + (size_t)i / columns, col = (size_t)i % columns;
+            out[i] = code_value(values, kind, (size_t)i) * scale_value(scale, scale_type, (row / block_rows) * columns + col);
+        }
+        break;
+    case ORC_SCALE_ROWS:
+#pragma omp parallel for schedule(static) if (n > (1L << 17))
+        for (long i = 0; i < n; ++i)
+            out[i] = code_value(values, kind, (size_t)i) * scale_value(scale, scale_type, first_row + (size_t)i / columns);
+        break;
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Epilogues in double.
+ * ------------------------------------------------------------------------------------------- */
+double orc_gelu_tanh(double x) {
+    const double c = sqrt(2.0 / M_PI);
+    return 0.5 * x * (1.0 + tanh(c * (x + 0.044715 * x * x * x)));
+}
+
+double orc_silu_glu(double gate, double up) { return gate / (1.0 + exp(-gate)) * up; }
+
+double orc_situ(double hidden, double gate) {
+    return (4.0 * tanh(gate / 4.0) * (1.0 / (1.0 + exp(-gate)))) * (25.0 * tanh(hidden / 25.0));
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * The truth: Sources/Siliconed/DiagnosticProbes.swift:74-178.
+ * ------------------------------------------------------------------------------------------- */
+void orc_sample_rows(int m, int count, int *rows) {
+    for (int i = 0; i < count; ++i) rows[i] = (int)(((int64_t)(2 * i + 1) * m) / (2 * count));
+}
+
+static double epilogue_one(int epilogue, const double *row, int j, int h) {
+    switch (epilogue) {
+    case ORC_EPI_GELU_TANH: return orc_gelu_tanh(row[j]);
+    case ORC_EPI_SILU_GLU: return orc_silu_glu(row[j], row[h + j]);
+    case ORC_EPI_SITU_GLU: return orc_situ(row[j], row[h + j]);
+    default: return row[j];
+    }
+}
+
+void orc_exact_rows(const int *rows, int nrows, const uint16_t *a, int64_t lda, const float *w,
+                    int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
+                    int epilogue, double *out) {
+    int glu = epilogue == ORC_EPI_SILU_GLU || epilogue == ORC_EPI_SITU_GLU;
+    int h = glu ? n / 2 : n;
+    double *prod = (double *)calloc((size_t)nrows * n, sizeof(double));
+    double *arow = (double *)malloc((size_t)nrows * k * sizeof(double));
+    for (int r = 0; r < nrows; ++r)
+        for (int kk = 0; kk < k; ++kk) arow[(size_t)r * k + kk] = orc_bf16_to_f32(a[(int64_t)rows[r] * lda + kk]);
+    if (w_kn) {
+        /* W [K, N]: each thread owns a block of columns and streams its K rows once. */
+        const int CB = 256;
+        int blocks = (n + CB - 1) / CB;
+#pragma omp parallel for schedule(dynamic)
+        for (int b = 0; b < blocks; ++b) {
+            int j0 = b * CB, j1 = j0 + CB < n ? j0 + CB : n;
+            for (int kk = 0; kk < k; ++kk) {
+                const float *wr = w + (int64_t)kk * ldw;
+                for (int r = 0; r < nrows; ++r) {
+                    double av = arow[(size_t)r * k + kk];
+                    double *pr = prod + (size_t)r * n;
+                    for (int j = j0; j < j1; ++j) pr[j] += av * (double)wr[j];
+                }
+            }
+        }
+    } else {
+#pragma omp parallel for schedule(dynamic)
+        for (int j = 0; j < n; ++j) {
+            const float *wr = w + (int64_t)j * ldw;
+            for (int r = 0; r < nrows; ++r) {
+                const double *ar = arow + (size_t)r * k;
+                double s = 0.0;
+                for (int kk = 0; kk < k; ++kk) s += ar[kk] * (double)wr[kk];
+                prod[(size_t)r * n + j] = s;
+            }
+        }
+    }
+    for (int r = 0; r < nrows; ++r) {
+        double *pr = prod + (size_t)r * n;
+        for (int j = 0; j < n; ++j) {
+            if (scale) pr[j] *= (double)scale[j];
+            if (bias) pr[j] += (double)bias[j];
+        }
+        for (int j = 0; j < h; ++j) out[(size_t)r * h + j] = epilogue_one(epilogue, pr, j, h);
+    }
+    free(prod);
+    free(arow);
+}
+
+/* Sources/Siliconed/DiagnosticJudgement.swift:39-71. */
+static int cmp_double(const void *x, const void *y) {
+    double a = *(const double *)x, b = *(const double *)y;
+    return (a > b) - (a < b);
+}
+
+double orc_channel_error(const float *got, const double *expected, int rows, int columns,
+                         int *worst_channel, double *median) {
+    double *num = (double *)calloc((size_t)columns, sizeof(double));
+    double *den = (double *)calloc((size_t)columns, sizeof(double));
+    double *norms = (double *)malloc((size_t)columns * sizeof(double));
+    double *live = (double *)malloc((size_t)columns * sizeof(double));
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < columns; ++c) {
+            size_t i = (size_t)r * columns + c;
+            double e = expected[i], d = (double)got[i] - e;
+            num[c] += d * d;
+            den[c] += e * e;
+        }
+    int nn = 0;
+    for (int c = 0; c < columns; ++c)
+        if (den[c] > 0) norms[nn++] = sqrt(den[c]);
+    double worst = 0.0, med = 0.0;
+    int channel = 0;
+    if (nn > 0) {
+        qsort(norms, (size_t)nn, sizeof(double), cmp_double);
+        double floor_ = 0.01 * norms[nn / 2];
+        int nl = 0;
+        for (int c = 0; c < columns; ++c) {
+            if (!(den[c] > 0)) continue;
+            double d = sqrt(den[c]);
+            double r = sqrt(num[c]) / (d > floor_ ? d : floor_);
+            if (isnan(r)) r = INFINITY;
+            live[nl++] = r;
+            if (r > worst) { worst = r; channel = c; }
+        }
+        qsort(live, (size_t)nl, sizeof(double), cmp_double);
+        med = live[nl / 2];
+    }
+    if (worst_channel) *worst_channel = channel;
+    if (median) *median = med;
+    free(num); free(den); free(norms); free(live);
+    return worst;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * The reference's fp32 epilogue passes: bias (Ops.swift:400-407, vDSP_vadd after the product),
+ * GELU-tanh in fp32 with tanhf (Ops.swift:386-398), SiLU gate (Ops.swift:64-94: −a, e^{−a},
+ * 1 + e^{−a}, a / (1 + e^{−a}), · b, each rounded), SITU in fp32 (MossImage.swift:889-900).
+ * ------------------------------------------------------------------------------------------- */
+void orc_epilogue_f32(const float *p, int64_t ldp, int m, int n, const float *bias, int epilogue,
+                      float *c, int64_t ldc, int threads) {
+    int glu = epilogue == ORC_EPI_SILU_GLU || epilogue == ORC_EPI_SITU_GLU;
+    int h = glu ? n / 2 : n;
+    const float gc = (float)sqrt(2.0 / M_PI);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+    for (int i = 0; i < m; ++i) {
+        const float *pr = p + (int64_t)i * ldp;
+        float *cr = c + (int64_t)i * ldc;
+        for (int j = 0; j < h; ++j) {
+            float v = pr[j];
+            if (bias) v = v + bias[j];
+            switch (epilogue) {
+            case ORC_EPI_GELU_TANH:
+                v = 0.5f * v * (1.0f + tanhf(gc * (v + 0.044715f * v * v * v)));
+                break;
+            case ORC_EPI_SILU_GLU: {
+                float u = pr[h + j];
+                if (bias) u = u + bias[h + j];
+                float e = expf(-v);
+                float s = 1.0f + e;
+                v = (v / s) * u;
+                break;
+            }
+            case ORC_EPI_SITU_GLU: {
+                float g = pr[h + j];
+                if (bias) g = g + bias[h + j];
+                float gate = 4.0f * tanhf(g / 4.0f) * (1.0f / (1.0f + expf(-g)));
+                float value = 25.0f * tanhf(v / 25.0f);
+                v = gate * value;
+                break;
+            }
+            default: break;
+            }
+            cr[j] = v;
+        }
+    }
+}

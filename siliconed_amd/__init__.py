@@ -1,0 +1,11 @@
+"""siliconed_amd — Siliconed's weight-quantized linear layer, MI355X-native (gfx950).
+
+int8 / fp8-e4m3 weights with per-output-channel fp32 scales × bf16 activations, fp32 sums in the
+matrix cores, fused scale + bias + GELU-tanh / SiLU-GLU / SITU-GLU epilogue, fused QKV. The work
+is done by the HIP library libsiliconed_q8.so (C ABI: include/siliconed_q8.h); this package holds
+its host side. There is no CPU fallback: without the library, importing the operators fails.
+"""
+from . import _abi as abi
+from .tensor_gemm import TensorGEMM, context, dequantize, linear, linear_qkv, round_bf16
+
+__all__ = ["abi", "TensorGEMM", "context", "linear", "linear_qkv", "dequantize", "round_bf16"]

@@ -1,0 +1,305 @@
+// sq8_api.hip — the C ABI (include/siliconed_q8.h) over the gfx950 kernels: argument checks,
+// the launch choice, GPU timing, status codes. No entry point aborts; none allocates per call
+// except the context's scratch for an fp32 activation, grown when a larger one arrives.
+#include "siliconed_q8.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <new>
+
+#include "sq8_gemm.h"
+
+struct sq8_ctx {
+    int device;
+    hipStream_t stream;
+    hipEvent_t begin, end;
+    void *scratch;          // bf16 copy of an fp32 activation (the reference's rounding scratch)
+    size_t scratch_bytes;
+};
+
+namespace {
+
+int hip_status(hipError_t e) { return e == hipSuccess ? SQ8_OK : -(int)e; }
+
+// Makes the context's device current for the scope, restoring the caller's afterwards.
+struct DeviceScope {
+    int previous = -1;
+    hipError_t error = hipSuccess;
+    explicit DeviceScope(int device) {
+        error = hipGetDevice(&previous);
+        if (error == hipSuccess && previous != device) error = hipSetDevice(device);
+    }
+    ~DeviceScope() {
+        int now = -1;
+        if (previous >= 0 && hipGetDevice(&now) == hipSuccess && now != previous) (void)hipSetDevice(previous);
+    }
+};
+
+bool aligned(const void *p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+bool is_glu(int epilogue) { return epilogue == SQ8_EPI_SILU_GLU || epilogue == SQ8_EPI_SITU_GLU; }
+
+int check_config(int a_dtype, int w_dtype, int w_layout, int scale_layout, int c_dtype, int epilogue) {
+    if (a_dtype != SQ8_BF16 && a_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    if (w_dtype != SQ8_INT8 && w_dtype != SQ8_FP8_E4M3) return SQ8_EUNSUPPORTED;
+    if (w_layout != SQ8_KN && w_layout != SQ8_NK) return SQ8_EINVAL;
+    if (scale_layout != SQ8_SCALE_TENSOR && scale_layout != SQ8_SCALE_COLUMNS) return SQ8_EUNSUPPORTED;
+    if (c_dtype != SQ8_BF16 && c_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    if (epilogue < SQ8_EPI_NONE || epilogue > SQ8_EPI_SITU_GLU) return SQ8_EINVAL;
+    return SQ8_OK;
+}
+
+// Grows the rounding scratch to `bytes` (never shrinks; freed with the context).
+int reserve_scratch(sq8_ctx *ctx, size_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return SQ8_OK;
+    if (ctx->scratch) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        e = hipFree(ctx->scratch);
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        if (e != hipSuccess) return hip_status(e);
+    }
+    hipError_t e = hipMalloc(&ctx->scratch, bytes);
+    if (e != hipSuccess) {
+        ctx->scratch = nullptr;
+        return hip_status(e);
+    }
+    ctx->scratch_bytes = bytes;
+    return SQ8_OK;
+}
+
+struct Product {
+    const void *a; int a_dtype; int64_t lda;
+    const void *w; int w_dtype; int w_layout; int64_t ldw;
+    const float *scale; int scale_layout; const float *bias; int epilogue;
+    void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
+    int m, k, n;
+};
+
+int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
+    if (!ctx) return SQ8_EINVAL;
+    int st = check_config(q.a_dtype, q.w_dtype, q.w_layout, q.scale_layout, q.c_dtype, q.epilogue);
+    if (st != SQ8_OK) return st;
+    if (q.m < 0 || q.k < 0 || q.n < 0) return SQ8_EINVAL;
+    if (is_glu(q.epilogue) && (q.n % 2) != 0) return SQ8_EINVAL;
+    const int n_out = is_glu(q.epilogue) ? q.n / 2 : q.n;
+    if (gpu_seconds) *gpu_seconds = 0.0;
+    if (q.m == 0 || n_out == 0) return SQ8_OK;
+    if (!q.a || !q.w || !q.scale || !q.c[0]) return SQ8_EINVAL;
+    if (q.lda < q.k || q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
+    if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
+
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+
+    sq8::GemmArgs p;
+    memset(&p, 0, sizeof(p));
+    p.lda = q.lda;
+    p.a = static_cast<const uint16_t *>(q.a);
+    if (gpu_seconds) {
+        hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    if (q.a_dtype == SQ8_F32) {
+        // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
+        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
+        if (st != SQ8_OK) return st;
+        const float *x = static_cast<const float *>(q.a);
+        uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
+        if (q.lda == q.k) {
+            hipError_t e = sq8::launch_round_bf16(x, y, (int64_t)q.m * q.k, ctx->stream);
+            if (e != hipSuccess) return hip_status(e);
+        } else {
+            for (int r = 0; r < q.m; ++r) {
+                hipError_t e = sq8::launch_round_bf16(x + (int64_t)r * q.lda, y + (int64_t)r * q.k, q.k, ctx->stream);
+                if (e != hipSuccess) return hip_status(e);
+            }
+        }
+        p.a = y;
+        p.lda = q.k;
+    }
+    p.w = static_cast<const uint8_t *>(q.w);
+    p.ldw = q.ldw;
+    p.scale = q.scale;
+    p.bias = q.bias;
+    p.c[0] = q.c[0];
+    p.c[1] = q.c[1];
+    p.c[2] = q.c[2];
+    p.ldc = q.ldc;
+    p.split = q.split;
+    p.head_dim = q.head_dim;
+    p.M = q.m;
+    p.N = q.n;
+    p.K = q.k;
+    p.glu_half = is_glu(q.epilogue) ? q.n / 2 : 0;
+    p.scale_per_col = q.scale_layout == SQ8_SCALE_COLUMNS;
+    p.a_vec = aligned(p.a, 16) && (p.lda % 8) == 0;
+    // [N, K]: 16-byte loads along K. [K, N]: 4-byte loads of 4 columns, which also needs the second
+    // half of a GLU weight to start on a multiple of 4.
+    p.w_vec = q.w_layout == SQ8_NK ? (aligned(p.w, 16) && (p.ldw % 16) == 0)
+                                   : (aligned(p.w, 4) && (p.ldw % 4) == 0 && (p.glu_half % 4) == 0);
+    const size_t esz = q.c_dtype == SQ8_F32 ? 4 : 2;
+    bool cv = true;
+    for (int i = 0; i < (q.split > 0 ? 3 : 1); ++i) cv = cv && aligned(q.c[i], 4 * esz);
+    if (q.head_dim > 0) cv = cv && (q.head_dim % 4) == 0;
+    else cv = cv && (q.ldc % 4) == 0;
+    p.c_vec = cv;
+
+    const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
+    const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
+    const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
+    const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
+    hipError_t e = sq8::launch_gemm(p, tile, wt, wl, q.epilogue, out, ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+    if (gpu_seconds) {
+        e = hipEventRecord(ctx->end, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->end);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->begin, ctx->end);
+        if (e != hipSuccess) return hip_status(e);
+        *gpu_seconds = (double)ms * 1e-3;
+    }
+    return SQ8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sq8_abi_version(void) { return SQ8_ABI_VERSION; }
+
+const char *sq8_status_string(int status) {
+    switch (status) {
+    case SQ8_OK: return "ok";
+    case SQ8_EINVAL: return "invalid argument";
+    case SQ8_EUNSUPPORTED: return "configuration not supported by this library";
+    case SQ8_ENODEVICE: return "no gfx950 device at that ordinal";
+    default: return status < 0 ? hipGetErrorString((hipError_t)(-status)) : "unknown status";
+    }
+}
+
+int sq8_create(int device, void *stream, sq8_ctx **out) {
+    if (!out) return SQ8_EINVAL;
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || device < 0 || device >= count) return SQ8_ENODEVICE;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_status(e);
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return SQ8_ENODEVICE;
+    DeviceScope scope(device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    sq8_ctx *ctx = new (std::nothrow) sq8_ctx;
+    if (!ctx) return SQ8_EINVAL;
+    memset(ctx, 0, sizeof(*ctx));
+    ctx->device = device;
+    ctx->stream = static_cast<hipStream_t>(stream);
+    e = hipEventCreate(&ctx->begin);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->end);
+    if (e != hipSuccess) {
+        if (ctx->begin) (void)hipEventDestroy(ctx->begin);
+        delete ctx;
+        return hip_status(e);
+    }
+    *out = ctx;
+    return SQ8_OK;
+}
+
+int sq8_destroy(sq8_ctx *ctx) {
+    if (!ctx) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    int st = SQ8_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) st = hip_status(e);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    (void)hipEventDestroy(ctx->begin);
+    (void)hipEventDestroy(ctx->end);
+    delete ctx;
+    return st;
+}
+
+int sq8_set_stream(sq8_ctx *ctx, void *stream) {
+    if (!ctx) return SQ8_EINVAL;
+    ctx->stream = static_cast<hipStream_t>(stream);
+    return SQ8_OK;
+}
+
+int sq8_supports(const sq8_ctx *ctx, int a_dtype, int w_dtype, int w_layout, int scale_layout, int c_dtype,
+                 int epilogue) {
+    if (!ctx) return SQ8_EINVAL;
+    return check_config(a_dtype, w_dtype, w_layout, scale_layout, c_dtype, epilogue);
+}
+
+int sq8_linear(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_dtype, int w_layout,
+               int64_t ldw, const float *scale, int scale_layout, const float *bias, int epilogue, void *c,
+               int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    Product q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda;
+    q.w = w; q.w_dtype = w_dtype; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_qkv(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_dtype, int w_layout,
+                   int64_t ldw, const float *scale, int scale_layout, const float *bias, void *q_out, void *k_out,
+                   void *v_out, int c_dtype, int64_t ldo, int head_dim, int m, int k, int d, double *gpu_seconds) {
+    if (d < 0 || (d % 4) != 0 || head_dim < 0) return SQ8_EINVAL;
+    if (head_dim > 0 && ((d % head_dim) != 0 || (head_dim % 4) != 0)) return SQ8_EINVAL;
+    if (head_dim == 0 && ldo < d) return SQ8_EINVAL;
+    if (d > 0 && (!q_out || !k_out || !v_out)) return SQ8_EINVAL;
+    if ((int64_t)3 * d > INT32_MAX) return SQ8_EINVAL;
+    Product q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda;
+    q.w = w; q.w_dtype = w_dtype; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = SQ8_EPI_NONE;
+    q.c[0] = q_out; q.c[1] = k_out; q.c[2] = v_out; q.c_dtype = c_dtype; q.ldc = ldo;
+    q.split = d; q.head_dim = head_dim;
+    q.m = m; q.k = k; q.n = 3 * d;
+    return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_dequantize(sq8_ctx *ctx, const void *codes, int w_dtype, int64_t rows, int64_t columns, const void *scale,
+                   int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out) {
+    if (!ctx) return SQ8_EINVAL;
+    if (w_dtype != SQ8_INT8 && w_dtype != SQ8_FP8_E4M3) return SQ8_EUNSUPPORTED;
+    if (rows < 0 || columns < 0 || first_row < 0) return SQ8_EINVAL;
+    if (rows == 0 || columns == 0) return SQ8_OK;
+    if (!codes || !out) return SQ8_EINVAL;
+    if (scale) {
+        if (scale_dtype != SQ8_F32 && scale_dtype != SQ8_BF16 && scale_dtype != SQ8_F16) return SQ8_EUNSUPPORTED;
+        if (scale_layout < SQ8_SCALE_TENSOR || scale_layout > SQ8_SCALE_ROWS) return SQ8_EINVAL;
+        if (scale_layout == SQ8_SCALE_BLOCKS && block_rows <= 0) return SQ8_EINVAL;
+    }
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_dequantize(static_cast<const uint8_t *>(codes),
+                                             w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8, rows, columns, scale,
+                                             scale_dtype, scale_layout, block_rows, first_row, out, ctx->stream));
+}
+
+int sq8_round_bf16(sq8_ctx *ctx, const float *x, uint16_t *y, int64_t count) {
+    if (!ctx || count < 0) return SQ8_EINVAL;
+    if (count == 0) return SQ8_OK;
+    if (!x || !y) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_round_bf16(x, y, count, ctx->stream));
+}
+
+int sq8_synchronize(sq8_ctx *ctx) {
+    if (!ctx) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(hipStreamSynchronize(ctx->stream));
+}
+
+}  // extern "C"

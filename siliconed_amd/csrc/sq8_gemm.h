@@ -1,0 +1,41 @@
+// sq8_gemm.h — host/device interface of the gfx950 weight-quantized GEMM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sq8_device.h"
+
+namespace sq8 {
+
+// One launch's operands; all pointers are device pointers.
+struct GemmArgs {
+    const uint16_t *a;      // bf16 [M, K], leading dimension lda (elements)
+    int64_t lda;
+    const uint8_t *w;       // codes: [K, N] (W_KN) or [N, K] (W_NK), leading dimension ldw
+    int64_t ldw;
+    const float *scale;     // fp32 [N] (scale_per_col) or [1]
+    const float *bias;      // fp32 [N] or null
+    void *c[3];             // outputs; c[1], c[2] only with `split`
+    int64_t ldc;
+    int split;              // > 0: output columns [i·split, (i+1)·split) go to c[i]
+    int head_dim;           // > 0: each output is [cols/head_dim, M, head_dim]
+    int M, N, K;            // N: weight columns (2h for a GLU epilogue)
+    int glu_half;           // h for GLU epilogues
+    int scale_per_col;
+    int a_vec, w_vec, c_vec; // 16-byte loads of A, wide loads of W, wide stores of C allowed
+    int tiles_m, tiles_n;   // set by the launcher
+};
+
+enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };
+
+int choose_tile(int M, int N_out, bool glu);
+hipError_t launch_gemm(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
+
+// Auxiliary kernels (sq8_aux.hip).
+hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t columns, const void *scale,
+                             int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out,
+                             hipStream_t stream);
+hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
+
+}  // namespace sq8

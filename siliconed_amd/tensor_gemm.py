@@ -1,0 +1,296 @@
+"""The host side of the weight-quantized linear layer, over the C ABI.
+
+`TensorGEMM` keeps the shape of the reference's operator (Sources/Siliconed/TensorGEMM.swift:59-360):
+`make` is `init?` (None where the library does not run: the caller keeps its widened route),
+`linear(a, int8=…, scales=…, per_column=…, c=…, m, k, n)` is `linear(a:int8:…:c:m:k:n:settled:)`
+and returns the GPU seconds (0 when `settled`, i.e. queued). The memory is torch's: tensors on the
+device are passed by their data pointers; torch is plumbing here, the product is the HIP library.
+
+The functional helpers below it (`linear`, `linear_qkv`, `dequantize`, `round_bf16`) allocate their
+outputs and are what the tests, the benchmark and the DiT block call.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _abi as abi
+
+_EPILOGUES = {
+    None: abi.EPI_NONE, "none": abi.EPI_NONE,
+    "gelu_tanh": abi.EPI_GELU_TANH, "gelu": abi.EPI_GELU_TANH,
+    "silu_glu": abi.EPI_SILU_GLU, "swiglu": abi.EPI_SILU_GLU,
+    "situ_glu": abi.EPI_SITU_GLU, "situ": abi.EPI_SITU_GLU,
+}
+_LAYOUTS = {"kn": abi.KN, "nk": abi.NK}
+
+
+def _epilogue(name) -> int:
+    if name not in _EPILOGUES:
+        raise ValueError(f"unknown epilogue {name!r}")
+    return _EPILOGUES[name]
+
+
+def _wdtype(w: torch.Tensor, fp8: Optional[bool]) -> int:
+    if w.dtype == torch.int8:
+        return abi.INT8
+    if w.dtype == getattr(torch, "float8_e4m3fn", None):
+        return abi.FP8_E4M3
+    if w.dtype == torch.uint8:
+        if fp8 is None:
+            raise ValueError("a uint8 weight needs fp8=True (e4m3fn codes) or an int8 view")
+        return abi.FP8_E4M3 if fp8 else abi.INT8
+    raise ValueError(f"weights must be int8 or float8_e4m3fn codes, not {w.dtype}")
+
+
+def _adtype(a: torch.Tensor) -> int:
+    if a.dtype == torch.bfloat16:
+        return abi.BF16
+    if a.dtype == torch.float32:
+        return abi.F32
+    raise ValueError(f"activations must be bfloat16 (or float32, rounded to bf16), not {a.dtype}")
+
+
+def _cdtype(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return abi.BF16
+    if dtype == torch.float32:
+        return abi.F32
+    raise ValueError(f"outputs are bfloat16 or float32, not {dtype}")
+
+
+def _dev(t: torch.Tensor, what: str) -> int:
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be on the GPU")
+    return t.data_ptr()
+
+
+def _row_major(t: torch.Tensor, what: str) -> int:
+    """Leading dimension of a 2-D tensor whose rows are contiguous."""
+    if t.dim() != 2 or (t.stride(1) != 1 and t.size(1) > 1):
+        raise ValueError(f"{what} must be 2-D with contiguous rows")
+    return t.stride(0) if t.size(0) > 1 else max(t.size(1), 1)
+
+
+class TensorGEMM:
+    """One context (device + stream) of the library: `TensorGEMM` of the reference."""
+
+    def __init__(self, handle: ctypes.c_void_p, device: int):
+        self._h = handle
+        self.device = device
+
+    @classmethod
+    def make(cls, device: int = 0, stream: Optional[torch.cuda.Stream] = None) -> Optional["TensorGEMM"]:
+        """`init?` (TensorGEMM.swift:206-232): None when the device is not a gfx950."""
+        lib = abi.load()
+        h = ctypes.c_void_p()
+        if stream is None and torch.cuda.is_available() and device < torch.cuda.device_count():
+            stream = torch.cuda.current_stream(device)
+        s = ctypes.c_void_p(stream.cuda_stream if stream is not None else None)
+        st = lib.sq8_create(device, s, ctypes.byref(h))
+        if st != abi.OK:
+            return None
+        return cls(h, device)
+
+    def close(self) -> None:
+        if self._h:
+            abi.check(abi.load().sq8_destroy(self._h), "sq8_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            if self._h:
+                abi.load().sq8_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+    def set_stream(self, stream: torch.cuda.Stream) -> None:
+        abi.check(abi.load().sq8_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)), "sq8_set_stream")
+
+    def synchronize(self) -> None:
+        abi.check(abi.load().sq8_synchronize(self._h), "sq8_synchronize")
+
+    def supports(self, a_dtype: int, w_dtype: int, layout: int, scale_layout: int, c_dtype: int, epilogue: int) -> bool:
+        return abi.load().sq8_supports(self._h, a_dtype, w_dtype, layout, scale_layout, c_dtype, epilogue) == abi.OK
+
+    # ---- the reference's entry point -----------------------------------------------------------
+
+    def linear(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
+               c: torch.Tensor, m: int, k: int, n: int, weight_offset: int = 0, scales_offset: int = 0,
+               block: Optional[int] = None, rotation=None, rounding: bool = True, quantizing=None,
+               settled: bool = False, layout: str = "kn", bias: Optional[torch.Tensor] = None,
+               epilogue=None, fp8: Optional[bool] = None) -> float:
+        """`linear(a:int8:weightOffset:scales:scalesOffset:perColumn:…:c:m:k:n:settled:)`
+        (TensorGEMM.swift:264-290): C[m, n] = A[m, k] · (q · s), q `[k, n]` (`layout="kn"`, the
+        map's) at `weight_offset` bytes into `int8`, its fp32 scales at `scales_offset` bytes into
+        `scales` (`n` of them, or one: `per_column` False). `a` fp32 is rounded to bf16 first when
+        `rounding` (the `rounding:` scratch route, TensorGEMMBF16.swift:208-264); `a` bf16 is
+        already rounded. Returns the GPU seconds, 0 when `settled` (queued).
+
+        Routes this library does not take raise `abi.Unsupported` before any work, as the
+        reference's `nil` pipelines send the caller back to the widened route: Q8_0 `block`
+        scales, convrot `rotation`, W8A8 `quantizing`, an fp32 activation not rounded.
+        """
+        if block is not None:
+            raise abi.Unsupported(abi.EUNSUPPORTED, "Q8_0 block scales")
+        if rotation is not None:
+            raise abi.Unsupported(abi.EUNSUPPORTED, "convrot rotation")
+        if quantizing is not None:
+            raise abi.Unsupported(abi.EUNSUPPORTED, "W8A8 activation quantization")
+        if a.dtype == torch.float32 and not rounding:
+            raise abi.Unsupported(abi.EUNSUPPORTED, "fp32 activations without bf16 rounding")
+        lay = _LAYOUTS[layout]
+        wd = _wdtype(int8, fp8)
+        epi = _epilogue(epilogue)
+        n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
+        if a.numel() < m * k or c.numel() < m * n_out:
+            raise ValueError("a or c smaller than m × k / m × n")
+        if int8.numel() * int8.element_size() < weight_offset + k * n:
+            raise ValueError("the weight buffer is smaller than its offset + k × n")
+        if scales.dtype != torch.float32 or scales.numel() * 4 < scales_offset + 4 * (n if per_column else 1):
+            raise ValueError("scales must be fp32, n of them (or one) after the offset")
+        if scales_offset % 4:
+            raise ValueError("the scales' offset must be a multiple of 4 bytes")
+        ldw = n if lay == abi.KN else k
+        secs = ctypes.c_double(0.0)
+        st = abi.load().sq8_linear(
+            self._h, _dev(a, "a"), _adtype(a), k,
+            _dev(int8, "int8") + weight_offset, wd, lay, ldw,
+            _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"), epi,
+            _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+            None if settled else ctypes.byref(secs))
+        abi.check(st, "sq8_linear")
+        return 0.0 if settled else secs.value
+
+    # ---- tensor-level operations ---------------------------------------------------------------
+
+    def product(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
+                bias: Optional[torch.Tensor] = None, epilogue=None, out: Optional[torch.Tensor] = None,
+                out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None,
+                timed: bool = False):
+        """y = act(s ⊙ (x · Wᵀ) + b) for x [m, k] and W [n, k] (`layout="nk"`, nn.Linear) or
+        [k, n] (`"kn"`, the map's). Returns y (and the GPU seconds when `timed`)."""
+        lay = _LAYOUTS[layout]
+        wd = _wdtype(w, fp8)
+        epi = _epilogue(epilogue)
+        if w.dim() != 2:
+            raise ValueError("w must be 2-D")
+        m, k = x.shape
+        n = w.shape[0] if lay == abi.NK else w.shape[1]
+        if (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
+            raise ValueError(f"x [{m}, {k}] and w {tuple(w.shape)} ({layout}) disagree on K")
+        glu = epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU)
+        if glu and n % 2:
+            raise ValueError("a GLU epilogue needs an even number of weight columns")
+        n_out = n // 2 if glu else n
+        per_col = scale.numel() != 1
+        if scale.dtype != torch.float32 or (per_col and scale.numel() != n):
+            raise ValueError("scale must be fp32 with n entries (or one)")
+        if bias is not None and (bias.dtype != torch.float32 or bias.numel() != n):
+            raise ValueError("bias must be fp32 with n entries")
+        if out is None:
+            out = torch.empty((m, n_out), dtype=out_dtype, device=x.device)
+        elif tuple(out.shape) != (m, n_out):
+            raise ValueError("out has the wrong shape")
+        secs = ctypes.c_double(0.0)
+        st = abi.load().sq8_linear(
+            self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
+            _dev(w, "w"), wd, lay, _row_major(w, "w"),
+            _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"), epi,
+            _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+            ctypes.byref(secs) if timed else None)
+        abi.check(st, "sq8_linear")
+        return (out, secs.value) if timed else out
+
+    def product_qkv(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
+                    bias: Optional[torch.Tensor] = None, head_dim: int = 0,
+                    out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None):
+        """Fused QKV: W of 3·d output channels; returns (q, k, v), each [m, d] (head_dim 0) or
+        [d/head_dim, m, head_dim]."""
+        lay = _LAYOUTS[layout]
+        wd = _wdtype(w, fp8)
+        m, k = x.shape
+        n = w.shape[0] if lay == abi.NK else w.shape[1]
+        if n % 3:
+            raise ValueError("a fused QKV weight has 3·d output channels")
+        d = n // 3
+        shape = (m, d) if head_dim == 0 else (d // head_dim, m, head_dim)
+        q, kk, v = (torch.empty(shape, dtype=out_dtype, device=x.device) for _ in range(3))
+        per_col = scale.numel() != 1
+        st = abi.load().sq8_linear_qkv(
+            self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
+            _dev(w, "w"), wd, lay, _row_major(w, "w"),
+            _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"),
+            q.data_ptr(), kk.data_ptr(), v.data_ptr(), _cdtype(out_dtype), d, head_dim, m, k, d, None)
+        abi.check(st, "sq8_linear_qkv")
+        return q, kk, v
+
+    def dequantize(self, codes: torch.Tensor, scale: Optional[torch.Tensor] = None, *,
+                   layout: int = abi.SCALE_COLUMNS, block_rows: int = 0, first_row: int = 0,
+                   fp8: Optional[bool] = None) -> torch.Tensor:
+        """Float(q)·s on the device (Widen.dequantize, Widen.swift:129-271); codes [rows, columns]."""
+        wd = _wdtype(codes, fp8)
+        codes2 = codes if codes.dim() == 2 else codes.reshape(1, -1)
+        rows, cols = codes2.shape
+        if not codes2.is_contiguous():
+            raise ValueError("codes must be contiguous")
+        out = torch.empty((rows, cols), dtype=torch.float32, device=codes.device)
+        sd = 0
+        if scale is not None:
+            sd = {torch.float32: abi.F32, torch.bfloat16: abi.BF16, torch.float16: abi.F16}.get(scale.dtype)
+            if sd is None:
+                raise ValueError("scales are fp32, bf16 or fp16")
+        st = abi.load().sq8_dequantize(self._h, codes2.data_ptr(), wd, rows, cols,
+                                       None if scale is None else _dev(scale, "scale"), sd, layout, block_rows,
+                                       first_row, out.data_ptr())
+        abi.check(st, "sq8_dequantize")
+        return out.reshape(codes.shape)
+
+    def round_bf16(self, x: torch.Tensor) -> torch.Tensor:
+        """fp32 → bf16 nearest-even (TensorGEMMBF16.swift:41-48)."""
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("x must be contiguous fp32")
+        y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        st = abi.load().sq8_round_bf16(self._h, x.data_ptr(), y.data_ptr(), x.numel())
+        abi.check(st, "sq8_round_bf16")
+        return y
+
+
+_contexts: dict = {}
+
+
+def context(device: Optional[int] = None) -> TensorGEMM:
+    """The default context of a device (on torch's current stream at creation)."""
+    if device is None:
+        device = torch.cuda.current_device()
+    ctx = _contexts.get(device)
+    if ctx is None:
+        ctx = TensorGEMM.make(device)
+        if ctx is None:
+            raise abi.Unsupported(abi.ENODEVICE, f"device {device} is not a gfx950")
+        _contexts[device] = ctx
+    ctx.set_stream(torch.cuda.current_stream(device))
+    return ctx
+
+
+def linear(x, w, scale, **kw):
+    """Functional form of `TensorGEMM.product` on the current device and stream."""
+    return context(x.device.index).product(x, w, scale, **kw)
+
+
+def linear_qkv(x, w, scale, **kw):
+    return context(x.device.index).product_qkv(x, w, scale, **kw)
+
+
+def dequantize(codes, scale=None, **kw):
+    return context(codes.device.index).dequantize(codes, scale, **kw)
+
+
+def round_bf16(x):
+    return context(x.device.index).round_bf16(x)

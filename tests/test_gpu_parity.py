@@ -1,0 +1,276 @@
+"""Parity of the HIP library (through its C ABI) with the CPU oracle, on an MI355X.
+
+Bars (the reference's own, Sources/Siliconed/Diagnostic.swift:105-107,
+CapacityProbes.swift:541-553): per-channel relative error (DiagnosticJudgement.swift:39-71) against
+the fp64 truth of the same bf16 activations and 8-bit codes ≤ 1e-5 for fp32 outputs, ≤ max(1e-5,
+1.25 × the error of the truth itself rounded to bf16) for bf16 outputs; plus, for bf16 outputs,
+max elementwise relative error ≤ 2e-2 with the denominator floored at 1 % of the column's RMS.
+Dequantised weights and the bf16 rounding pass are compared bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from refgen import DequantizeGen, bitwise_equal, code_values
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+EPI = {"none": 0, "gelu": 1, "silu": 2, "situ": 3}
+
+
+def bf16_dev(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def dev(x: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def problem(orc, m, k, n, fp8, seed, bias=True):
+    """bf16 X ~ N(0,1); int8 codes uniform in [−127, 127] with scales U(1e−3, 2e−2), or fp8 codes of
+    N(0, 0.02) weights with amax/448 scales; bias N(0, 0.02). Codes laid out [N, K]."""
+    x = orc.normal_bf16(seed, (m, k))
+    if fp8:
+        q, s = orc.quantize_fp8_per_row(orc.normal_f32(seed + 1, (n, k), 0.0, 0.02))
+    else:
+        q = orc.uniform_i8(seed + 1, (n, k)).view(np.uint8)
+        s = orc.uniform_f32(seed + 2, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(seed + 3, (n,), 0.0, 0.02) if bias else None
+    return x, q, s, b
+
+
+def weight_tensor(q: np.ndarray, fp8: bool, layout: str) -> torch.Tensor:
+    w = q if layout == "nk" else np.ascontiguousarray(q.T)
+    t = dev(w)
+    return t.view(torch.float8_e4m3fn) if fp8 else t.view(torch.int8)
+
+
+def judge(orc, got, x, q, fp8, s, b, epi, out_dtype, rows=None):
+    m, k = x.shape
+    n = q.shape[0]
+    rows = np.arange(m, dtype=np.int32) if rows is None else rows
+    wf = code_values(q, fp8)
+    exact = orc.exact_rows(rows, x, wf, False, k, n, scale=s, bias=b, epilogue=EPI[epi])
+    g = got[rows]
+    assert np.isfinite(g).all(), "non-finite outputs"
+    err, ch, _ = orc.channel_error(g, exact)
+    if out_dtype == torch.bfloat16:
+        floor = orc.channel_error(orc.bf16_to_f32(orc.f32_to_bf16(exact.astype(np.float32))), exact)[0]
+        bar = max(1e-5, 1.25 * floor)
+        rms = np.sqrt((exact ** 2).mean(axis=0)) + 1e-30
+        rel = np.abs(g - exact) / np.maximum(np.abs(exact), 0.01 * rms)
+        assert rel.max() <= 2e-2, f"max relative error {rel.max():.3e}"
+    else:
+        bar = 1e-5
+    assert err <= bar, f"channelError {err:.3e} > {bar:.3e} (channel {ch})"
+    return err
+
+
+def run(gemm, x, q, s, b, fp8, layout, epi, out_dtype):
+    w = weight_tensor(q, fp8, layout)
+    y = gemm.product(bf16_dev(x), w, dev(s), layout=layout, bias=None if b is None else dev(b),
+                     epilogue=None if epi == "none" else {"gelu": "gelu_tanh", "silu": "silu_glu", "situ": "situ_glu"}[epi],
+                     out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+# ---- conversions on the device, bit for bit ------------------------------------------------------
+
+def test_fp8_codes_widen_exactly(gemm, orc):
+    codes = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    got = gemm.dequantize(dev(codes), None, fp8=True).cpu().numpy()
+    assert bitwise_equal(got, orc.e4m3_table().reshape(1, 256)) == 0
+    assert bitwise_equal(got, code_values(codes, True)) == 0
+
+
+def test_int8_codes_widen_exactly(gemm):
+    codes = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    got = gemm.dequantize(dev(codes).view(torch.int8), None).cpu().numpy()
+    assert bitwise_equal(got, codes.view(np.int8).astype(np.float32)) == 0
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_dequantize_reference_vectors(gemm, fp8):
+    """DequantizeTests.swift:79-133 on the device: columns, tensor, blocks (mid-block), rows."""
+    from siliconed_amd import abi
+    g = DequantizeGen()
+    view = (lambda t: t) if fp8 else (lambda t: t.view(torch.int8))
+    k, n = 300, 500
+    q = g.codes(k * n).reshape(k, n)
+    for kind, dt in [("bf16", torch.bfloat16), ("f32", torch.float32), ("f16", torch.float16)]:
+        raw, s = g.scales(n, kind)
+        sd = dev(raw.view(np.int16)).view(dt) if kind != "f32" else dev(raw)
+        got = gemm.dequantize(view(dev(q)), sd, layout=abi.SCALE_COLUMNS, fp8=fp8 or None).cpu().numpy()
+        assert bitwise_equal(got, code_values(q, fp8) * s[None, :]) == 0
+    raw, s = g.scales(4, "f32")
+    got = gemm.dequantize(view(dev(q)), dev(raw[:1]), layout=abi.SCALE_TENSOR, fp8=fp8 or None).cpu().numpy()
+    assert bitwise_equal(got, code_values(q, fp8) * s[0]) == 0
+    kb, nb, b = 100, 2052, 32
+    qb = g.codes(kb * nb).reshape(kb, nb)
+    raw, s = g.scales((kb + b - 1) // b * nb, "bf16")
+    sd = dev(raw.view(np.int16)).view(torch.bfloat16)
+    first, rows = 45, 50
+    got = gemm.dequantize(view(dev(qb[first:first + rows])), sd, layout=abi.SCALE_BLOCKS, block_rows=b,
+                          first_row=first, fp8=fp8 or None).cpu().numpy()
+    r = np.arange(rows)[:, None] + first
+    want = code_values(qb[first:first + rows], fp8) * s[(r // b) * nb + np.arange(nb)[None, :]]
+    assert bitwise_equal(got, want) == 0
+    rr, kk = 250, 600
+    qr = g.codes(rr * kk).reshape(rr, kk)
+    raw, s = g.scales(rr + 7, "bf16")
+    sd = dev(raw.view(np.int16)).view(torch.bfloat16)
+    got = gemm.dequantize(view(dev(qr)), sd, layout=abi.SCALE_ROWS, first_row=7, fp8=fp8 or None).cpu().numpy()
+    assert bitwise_equal(got, code_values(qr, fp8) * s[7:7 + rr, None]) == 0
+
+
+def test_round_bf16_bits(gemm, orc):
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 2 ** 32, size=1 << 16, dtype=np.uint64).astype(np.uint32)
+    u[:8] = [0x7F800001, 0xFF800001, 0x7FC00000, 0x7F7FFFFF, 0x3F808000, 0x3F818000, 0x00000001, 0x80000000]
+    x = u.view(np.float32)
+    got = gemm.round_bf16(dev(x)).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, orc.f32_to_bf16(x))
+
+
+# ---- the product ---------------------------------------------------------------------------------
+
+SHAPES = [
+    (256, 3072, 3072),      # config 0's K and N, rows reduced
+    (150, 768, 96),         # the reference's kernel-test shapes (W8A8KernelTests.swift:74-83)
+    (70, 10240, 72),
+    (65, 448, 130),
+    (33, 520, 40),
+    (1, 16, 8),
+    (300, 200, 1000),
+]
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_product_shapes(gemm, orc, shape, layout, fp8):
+    m, k, n = shape
+    x, q, s, b = problem(orc, m, k, n, fp8, seed=100 + m + k + n)
+    for out in (torch.float32, torch.bfloat16):
+        got = run(gemm, x, q, s, b, fp8, layout, "none", out)
+        judge(orc, got, x, q, fp8, s, b, "none", out)
+
+
+@pytest.mark.parametrize("epi", ["gelu", "silu", "situ"])
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_product_epilogues(gemm, orc, epi, fp8, layout):
+    for m, k, n in [(256, 1024, 768), (65, 448, 130)]:
+        x, q, s, b = problem(orc, m, k, n, fp8, seed=7 + n)
+        for out in (torch.float32, torch.bfloat16):
+            got = run(gemm, x, q, s, b, fp8, layout, epi, out)
+            judge(orc, got, x, q, fp8, s, b, epi, out)
+
+
+def test_zero_row_and_massive_column(gemm, orc):
+    # W8A8KernelTests.swift:164-168: a zero row, a ×300 activation column.
+    m, k, n = 96, 512, 256
+    x, q, s, b = problem(orc, m, k, n, False, seed=5)
+    xf = orc.bf16_to_f32(x)
+    xf[10, :] = 0.0
+    xf[:, 77] *= 300.0
+    x = orc.f32_to_bf16(xf)
+    got = run(gemm, x, q, s, b, False, "kn", "none", torch.float32)
+    assert np.array_equal(got[10], b)  # 0·s + b exactly
+    judge(orc, got, x, q, False, s, b, "none", torch.float32)
+
+
+def test_scale_after_the_sum_and_tensor_scale(gemm, orc):
+    m, k, n = 128, 1024, 384
+    x, q, s, _ = problem(orc, m, k, n, False, seed=9, bias=False)
+    st = np.float32(0.0123)
+    w = weight_tensor(q, False, "nk")
+    a = gemm.product(bf16_dev(x), w, dev(np.array([st])), layout="nk", out_dtype=torch.float32)
+    c = gemm.product(bf16_dev(x), w, dev(np.full(n, st, np.float32)), layout="nk", out_dtype=torch.float32)
+    assert torch.equal(a, c)
+    # Power-of-two scales commute with the fp32 sum exactly: y(2s) = 2·y(s) bit for bit.
+    y1 = gemm.product(bf16_dev(x), w, dev(s), layout="nk", out_dtype=torch.float32)
+    y2 = gemm.product(bf16_dev(x), w, dev(2 * s), layout="nk", out_dtype=torch.float32)
+    assert torch.equal(2 * y1, y2)
+
+
+def test_rows_and_columns_are_independent(gemm, orc):
+    # Any chunking of rows gives the same rows (WeightProducts.swift:524-528); the first columns of
+    # a wider weight are that weight's columns (`submit(…columns:)`, TensorGEMM.swift:296).
+    m, k, n = 600, 768, 512
+    x, q, s, b = problem(orc, m, k, n, False, seed=11)
+    w = weight_tensor(q, False, "kn")
+    xt, st, bt = bf16_dev(x), dev(s), dev(b)
+    whole = gemm.product(xt, w, st, layout="kn", bias=bt, out_dtype=torch.float32)
+    part = gemm.product(xt[123:400], w, st, layout="kn", bias=bt, out_dtype=torch.float32)
+    assert torch.equal(part, whole[123:400])
+    c = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    secs = gemm.linear(xt, int8=w, scales=st, per_column=True, c=c, m=m, k=k, n=n, layout="kn", bias=bt)
+    assert secs > 0.0 and torch.equal(c, whole)
+    cols = 200
+    # n = cols with ldw = n of the full weight: the C ABI called directly with the wider stride.
+    from siliconed_amd import _abi as abi
+    import ctypes
+    c2 = torch.empty((m, cols), dtype=torch.float32, device=DEV)
+    st_ = abi.load().sq8_linear(gemm._h, xt.data_ptr(), abi.BF16, k, w.data_ptr(), abi.INT8, abi.KN, n,
+                                st.data_ptr(), abi.SCALE_COLUMNS, bt.data_ptr(), abi.EPI_NONE, c2.data_ptr(), abi.F32,
+                                cols, m, k, cols, None)
+    assert st_ == 0
+    torch.cuda.synchronize()
+    assert torch.equal(c2, whole[:, :cols])
+
+
+def test_fp32_activation_is_rounded_first(gemm, orc):
+    m, k, n = 200, 640, 320
+    x32 = orc.normal_f32(21, (m, k))
+    q = orc.uniform_i8(22, (n, k)).view(np.uint8)
+    s = orc.uniform_f32(23, (n,), 1e-3, 2e-2)
+    w = weight_tensor(q, False, "nk")
+    a = gemm.product(dev(x32), w, dev(s), layout="nk", out_dtype=torch.float32)
+    r = gemm.product(bf16_dev(orc.f32_to_bf16(x32)), w, dev(s), layout="nk", out_dtype=torch.float32)
+    assert torch.equal(a, r)
+
+
+@pytest.mark.parametrize("head_dim", [0, 128])
+def test_fused_qkv(gemm, orc, head_dim):
+    m, k, d = 300, 1024, 512
+    x, q, s, b = problem(orc, m, k, 3 * d, False, seed=31)
+    w = weight_tensor(q, False, "nk")
+    whole = gemm.product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), out_dtype=torch.bfloat16)
+    qq, kk, vv = gemm.product_qkv(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), head_dim=head_dim)
+    for i, t in enumerate((qq, kk, vv)):
+        part = whole[:, i * d:(i + 1) * d]
+        if head_dim:
+            part = part.reshape(m, d // head_dim, head_dim).permute(1, 0, 2)
+        assert torch.equal(t, part)
+
+
+def test_empty_and_refused(gemm):
+    from siliconed_amd import abi
+    x = torch.zeros((0, 64), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((32, 64), dtype=torch.int8, device=DEV)
+    s = torch.ones(32, dtype=torch.float32, device=DEV)
+    assert gemm.product(x, w, s).shape == (0, 32)
+    with pytest.raises(abi.Unsupported):
+        gemm.linear(x, int8=w, scales=s, per_column=True, c=torch.empty(0, device=DEV), m=0, k=64, n=32, block=32)
+    with pytest.raises(ValueError):
+        gemm.product(torch.zeros((4, 63), dtype=torch.bfloat16, device=DEV), w, s)
+
+
+# ---- the baseline's shapes, on sampled rows ----------------------------------------------------
+
+@pytest.mark.parametrize("case", ["c1_up_gelu", "c1_down", "c2_qkv", "c2_text", "c3_gate_up_fp8", "c3_down_fp8"])
+def test_baseline_shapes_sampled_rows(gemm, orc, case):
+    m, k, n, fp8, epi = {
+        "c1_up_gelu": (4096, 3072, 12288, False, "gelu"),
+        "c1_down": (4096, 12288, 3072, False, "none"),
+        "c2_qkv": (4608, 3072, 9216, False, "none"),
+        "c2_text": (512, 3072, 3072, False, "none"),
+        "c3_gate_up_fp8": (4096, 3840, 20480, True, "silu"),
+        "c3_down_fp8": (4096, 10240, 3840, True, "none"),
+    }[case]
+    x, q, s, b = problem(orc, m, k, n, fp8, seed=1000 + k)
+    for layout in ("kn", "nk"):
+        got = run(gemm, x, q, s, b, fp8, layout, epi, torch.bfloat16)
+        judge(orc, got, x, q, fp8, s, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
