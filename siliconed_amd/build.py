@@ -17,7 +17,18 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libsiliconed_q8.so")
-SOURCES = ["sq8_gemm.hip", "sq8_aux.hip", "sq8_api.hip"]
+# (source, object name, extra defines): the FAST kernel set is one source compiled per weight type
+# and layout, so the sets compile in parallel.
+SOURCES = [
+    ("sq8_gemm.hip", "sq8_gemm", []),
+    ("sq8_gemm_general.hip", "sq8_gemm_general", []),
+    ("sq8_gemm_inst.hip", "sq8_gemm_i8_kn", ["-DSQ8_WT=0", "-DSQ8_WL=0"]),
+    ("sq8_gemm_inst.hip", "sq8_gemm_i8_nk", ["-DSQ8_WT=0", "-DSQ8_WL=1"]),
+    ("sq8_gemm_inst.hip", "sq8_gemm_f8_kn", ["-DSQ8_WT=1", "-DSQ8_WL=0"]),
+    ("sq8_gemm_inst.hip", "sq8_gemm_f8_nk", ["-DSQ8_WT=1", "-DSQ8_WL=1"]),
+    ("sq8_aux.hip", "sq8_aux", []),
+    ("sq8_api.hip", "sq8_api", []),
+]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -34,9 +45,10 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(item) -> str:
+    src, name, defines = item
+    obj = os.path.join(OBJ, name + ".o")
+    cmd = [HIPCC, *FLAGS, *defines, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

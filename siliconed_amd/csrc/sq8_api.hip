@@ -153,7 +153,10 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
     const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
-    hipError_t e = sq8::launch_gemm(p, tile, wt, wl, q.epilogue, out, ctx->stream);
+    const int cols_per_half = is_glu(q.epilogue) ? q.n / 2 : q.n;
+    const bool fast = p.a_vec && p.w_vec && q.k > 0 && (q.k % 64) == 0 && cols_per_half >= 4 &&
+                      (q.w_layout == SQ8_NK || (cols_per_half % 4) == 0);
+    hipError_t e = sq8::launch_gemm(p, fast, tile, wt, wl, q.epilogue, out, ctx->stream);
     if (e != hipSuccess) return hip_status(e);
     if (gpu_seconds) {
         e = hipEventRecord(ctx->end, ctx->stream);

@@ -30,7 +30,10 @@ struct GemmArgs {
 enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };
 
 int choose_tile(int M, int N_out, bool glu);
-hipError_t launch_gemm(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
+// `fast`: the branch-free kernels, valid when A rows and W rows/columns can be read with vector
+// loads (alignment), K is a positive multiple of 64, and there are at least 4 weight columns (per
+// GLU half) with a [K, N] weight's column count a multiple of 4.
+hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
 
 // Auxiliary kernels (sq8_aux.hip).
 hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t columns, const void *scale,
