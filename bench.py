@@ -101,7 +101,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--layout", choices=["kn", "nk"], default="kn")
+    ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
+                    help="weight layout the product reads; packed = staged once from [K, N] by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -114,16 +115,24 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     x, q_kn, s, b = inputs()
-    q = q_kn if args.layout == "kn" else np.ascontiguousarray(q_kn.T)
+    q = np.ascontiguousarray(q_kn.T) if args.layout == "nk" else q_kn
     xd = x.to(dev)
     wd = torch.from_numpy(q).to(dev)
     sd = torch.from_numpy(s).to(dev)
     bd = torch.from_numpy(b).to(dev)
     out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ctx = sq.context(0)
+    stage_ms = None
+    if args.layout == "packed":
+        torch.cuda.synchronize()
+        t_stage = time.perf_counter()
+        wd = ctx.pack(wd, layout="kn")
+        torch.cuda.synchronize()
+        stage_ms = 1e3 * (time.perf_counter() - t_stage)
+    layout = "nk" if args.layout == "nk" else "kn"
 
     def step():
-        ctx.product(xd, wd, sd, layout=args.layout, bias=bd, epilogue="gelu_tanh", out=out)
+        ctx.product(xd, wd, sd, layout=layout, bias=bd, epilogue="gelu_tanh", out=out)
 
     for _ in range(args.warmup):
         step()
@@ -157,7 +166,8 @@ def main() -> int:
         "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}",
         "config": {"workload": "C1 up-projection: int8 weight [K,N] per-channel fp32 scale, bf16 X, bias + fused "
                                "GELU-tanh, bf16 out",
-                   "M": M, "K": K, "N": N, "weight_layout": args.layout.upper(), "global_batch": M,
+                   "M": M, "K": K, "N": N, "weight_layout": args.layout.upper(),
+                   "staging_ms": None if stage_ms is None else round(stage_ms, 3), "global_batch": M,
                    "parallelism": "none (one GPU)"},
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kernel_ms, 5),

@@ -53,6 +53,9 @@ enum sq8_wlayout {
     SQ8_KN = 0,            /* [K, N] row-major, N contiguous: the map's layout
                               (`linear_weights_transposed`, Artifact.swift:655) */
     SQ8_NK = 1,            /* [N, K] row-major, K contiguous: a published nn.Linear */
+    SQ8_PACKED = 2,        /* sq8_pack_weight's layout (glu = 0); `ldw` is ignored */
+    SQ8_PACKED_GLU = 3,    /* sq8_pack_weight's layout of a [first half | second half] GLU weight
+                              (glu = 1), for the GLU epilogues only */
 };
 
 /* ---- scale layouts (Widen.ScaleLayout, Sources/Siliconed/Widen.swift:100-110) ---- */
@@ -116,6 +119,21 @@ int sq8_linear(sq8_ctx *ctx,
                const float *bias, int epilogue,
                void *c, int c_dtype, int64_t ldc,
                int m, int k, int n, double *gpu_seconds);
+
+/* Bytes of the packed layout of a weight of k × n codes (GLU: n = 2h, the halves paired).
+ * Replaces: the reserve plan's size of the staged integers (WeightProducts.int8Plan,
+ * Sources/Siliconed/WeightProducts.swift:535-600). */
+int64_t sq8_packed_bytes(int k, int n, int glu);
+
+/* **Staging**: rewrites the codes of a weight (`w_layout` SQ8_KN or SQ8_NK, leading dimension
+ * `ldw`, k × n codes) into the layout the product streams fastest — per 64-column slab, per step
+ * of 64 K, per lane, 16 contiguous bytes, zero-padded — into `out` (sq8_packed_bytes bytes, device
+ * memory the caller owns). Once per weight, before its products; the bytes are the same codes
+ * (no widening, the scales untouched). `glu` = 1 pairs the two halves of a gate-up weight for the
+ * GLU epilogues. Queued on the context's stream.
+ * Replaces: Artifact.stageInt8, the copy of q and its scales into the model's reserve
+ * (Sources/Siliconed/Artifact.swift:755-774), for the packed route. */
+int sq8_pack_weight(sq8_ctx *ctx, const void *w, int w_layout, int64_t ldw, int k, int n, int glu, void *out);
 
 /* **The fused QKV product**: one product of n = 3·d columns whose output columns [0,d), [d,2d),
  * [2d,3d) go to `q`, `k`, `v`. `head_dim` = 0: each output is [m, d] row-major (leading

@@ -6,6 +6,6 @@ is done by the HIP library libsiliconed_q8.so (C ABI: include/siliconed_q8.h); t
 its host side. There is no CPU fallback: without the library, importing the operators fails.
 """
 from . import _abi as abi
-from .tensor_gemm import TensorGEMM, context, dequantize, linear, linear_qkv, round_bf16
+from .tensor_gemm import PackedWeight, TensorGEMM, context, dequantize, linear, linear_qkv, pack, round_bf16
 
-__all__ = ["abi", "TensorGEMM", "context", "linear", "linear_qkv", "dequantize", "round_bf16"]
+__all__ = ["abi", "PackedWeight", "TensorGEMM", "context", "linear", "linear_qkv", "pack", "dequantize", "round_bf16"]

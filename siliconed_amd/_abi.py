@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(PKG, "libsiliconed_q8.so")
 # Values of include/siliconed_q8.h.
 OK, EINVAL, EUNSUPPORTED, ENODEVICE = 0, 1, 2, 3
 BF16, F32, INT8, FP8_E4M3, F16 = 1, 2, 3, 4, 5
-KN, NK = 0, 1
+KN, NK, PACKED, PACKED_GLU = 0, 1, 2, 3
 SCALE_TENSOR, SCALE_COLUMNS, SCALE_BLOCKS, SCALE_ROWS = 0, 1, 2, 3
 EPI_NONE, EPI_GELU_TANH, EPI_SILU_GLU, EPI_SITU_GLU = 0, 1, 2, 3
 
@@ -29,6 +29,8 @@ SIGNATURES = {
                         ctypes.POINTER(_D)]),
     "sq8_linear_qkv": (_I, [_P, _P, _I, _I64, _P, _I, _I, _I64, _P, _I, _P, _P, _P, _P, _I, _I64, _I, _I, _I, _I,
                             ctypes.POINTER(_D)]),
+    "sq8_packed_bytes": (_I64, [_I, _I, _I]),
+    "sq8_pack_weight": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P]),
     "sq8_dequantize": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _I, _I64, _I64, _P]),
     "sq8_round_bf16": (_I, [_P, _P, _P, _I64]),
     "sq8_synchronize": (_I, [_P]),

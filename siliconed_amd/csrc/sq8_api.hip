@@ -41,10 +41,13 @@ bool aligned(const void *p, size_t bytes) { return (reinterpret_cast<uintptr_t>(
 
 bool is_glu(int epilogue) { return epilogue == SQ8_EPI_SILU_GLU || epilogue == SQ8_EPI_SITU_GLU; }
 
+bool is_packed(int w_layout) { return w_layout == SQ8_PACKED || w_layout == SQ8_PACKED_GLU; }
+
 int check_config(int a_dtype, int w_dtype, int w_layout, int scale_layout, int c_dtype, int epilogue) {
     if (a_dtype != SQ8_BF16 && a_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
     if (w_dtype != SQ8_INT8 && w_dtype != SQ8_FP8_E4M3) return SQ8_EUNSUPPORTED;
-    if (w_layout != SQ8_KN && w_layout != SQ8_NK) return SQ8_EINVAL;
+    if (w_layout < SQ8_KN || w_layout > SQ8_PACKED_GLU) return SQ8_EINVAL;
+    if (is_packed(w_layout) && (w_layout == SQ8_PACKED_GLU) != is_glu(epilogue)) return SQ8_EINVAL;
     if (scale_layout != SQ8_SCALE_TENSOR && scale_layout != SQ8_SCALE_COLUMNS) return SQ8_EUNSUPPORTED;
     if (c_dtype != SQ8_BF16 && c_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
     if (epilogue < SQ8_EPI_NONE || epilogue > SQ8_EPI_SITU_GLU) return SQ8_EINVAL;
@@ -89,7 +92,8 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (gpu_seconds) *gpu_seconds = 0.0;
     if (q.m == 0 || n_out == 0) return SQ8_OK;
     if (!q.a || !q.w || !q.scale || !q.c[0]) return SQ8_EINVAL;
-    if (q.lda < q.k || q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
+    if (q.lda < q.k) return SQ8_EINVAL;
+    if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
 
     DeviceScope scope(ctx->device);
@@ -150,13 +154,25 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     p.c_vec = cv;
 
     const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
-    const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
-    const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
     const int cols_per_half = is_glu(q.epilogue) ? q.n / 2 : q.n;
-    const bool fast = p.a_vec && p.w_vec && q.k > 0 && (q.k % 64) == 0 && cols_per_half >= 4 &&
-                      (q.w_layout == SQ8_NK || (cols_per_half % 4) == 0);
-    hipError_t e = sq8::launch_gemm(p, fast, tile, wt, wl, q.epilogue, out, ctx->stream);
+    const bool k_steps = q.k > 0 && (q.k % 64) == 0;
+    p.kt = (q.k + 63) / 64;
+    hipError_t e;
+    if (is_packed(q.w_layout) || (q.w_layout == SQ8_NK && p.a_vec && p.w_vec && k_steps && cols_per_half >= 1)) {
+        // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
+        if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
+        const int wl = is_packed(q.w_layout) ? sq8::W_PACKED : sq8::W_NK;
+        const long tiles256 = (long)((q.m + 255) / 256) * ((q.n + 255) / 256);
+        const int tile = tiles256 >= 160 ? sq8::WD_256 : sq8::WD_128;
+        e = sq8::launch_wdirect(p, tile, wt, wl, q.epilogue, out, ctx->stream);
+    } else {
+        const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
+        const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
+        const bool fast = p.a_vec && p.w_vec && k_steps && cols_per_half >= 4 &&
+                          (q.w_layout == SQ8_NK || (cols_per_half % 4) == 0);
+        e = sq8::launch_gemm(p, fast, tile, wt, wl, q.epilogue, out, ctx->stream);
+    }
     if (e != hipSuccess) return hip_status(e);
     if (gpu_seconds) {
         e = hipEventRecord(ctx->end, ctx->stream);
@@ -268,6 +284,23 @@ int sq8_linear_qkv(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const 
     q.split = d; q.head_dim = head_dim;
     q.m = m; q.k = k; q.n = 3 * d;
     return run_product(ctx, q, gpu_seconds);
+}
+
+int64_t sq8_packed_bytes(int k, int n, int glu) {
+    if (k < 0 || n < 0 || (glu && (n % 2) != 0)) return -1;
+    return sq8::packed_bytes(k, n, glu != 0);
+}
+
+int sq8_pack_weight(sq8_ctx *ctx, const void *w, int w_layout, int64_t ldw, int k, int n, int glu, void *out) {
+    if (!ctx || k < 0 || n < 0 || (glu && (n % 2) != 0)) return SQ8_EINVAL;
+    if (w_layout != SQ8_KN && w_layout != SQ8_NK) return SQ8_EINVAL;
+    if (ldw < (w_layout == SQ8_KN ? n : k)) return SQ8_EINVAL;
+    if (k == 0 || n == 0) return SQ8_OK;
+    if (!w || !out) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_pack(static_cast<const uint8_t *>(w), w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK, ldw,
+                                       k, n, glu != 0, static_cast<uint8_t *>(out), ctx->stream));
 }
 
 int sq8_dequantize(sq8_ctx *ctx, const void *codes, int w_dtype, int64_t rows, int64_t columns, const void *scale,

@@ -57,7 +57,55 @@ int grid_for(int64_t count) {
     return (int)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192);
 }
 
+// One thread per 16-byte chunk of the packed layout: chunk c = ((slab·kt + t)·4 + j)·64 + lane holds
+// codes k ∈ [64t + 32h + 16(j&1), +16) of virtual column 32·(j>>1) + (lane & 31) of the slab
+// (h = lane >> 5); virtual columns are the weight's own, or for GLU the slab's 32 output columns of
+// the first half then the same of the second. Zeros past K and past the columns.
+__global__ void __launch_bounds__(256) pack_kernel(const uint8_t *__restrict__ w, int wl, int64_t ldw, int k, int n,
+                                                   int glu, int kt, int64_t chunks, uint8_t *__restrict__ out) {
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(c & 63), j = (int)((c >> 6) & 3);
+        const int64_t st = c >> 8;
+        const int t = (int)(st % kt), slab = (int)(st / kt);
+        const int b = j >> 1, h = lane >> 5, nl = lane & 31;
+        int col;
+        bool valid;
+        if (glu) {
+            const int half = n / 2, oc = slab * 32 + nl;
+            valid = oc < half;
+            col = oc + b * half;
+        } else {
+            col = slab * 64 + b * 32 + nl;
+            valid = col < n;
+        }
+        const int k0 = 64 * t + 32 * h + 16 * (j & 1);
+        uint32_t d[4] = {0, 0, 0, 0};
+        for (int e = 0; e < 16; ++e) {
+            const int kk = k0 + e;
+            uint32_t v = 0;
+            if (valid && kk < k) v = wl == W_KN ? w[(int64_t)kk * ldw + col] : w[(int64_t)col * ldw + kk];
+            d[e >> 2] |= v << (8 * (e & 3));
+        }
+        *reinterpret_cast<u32x4 *>(out + c * 16) = u32x4{d[0], d[1], d[2], d[3]};
+    }
+}
+
 }  // namespace
+
+int64_t packed_bytes(int k, int n, bool glu) {
+    const int64_t kt = (k + 63) / 64;
+    const int64_t slabs = glu ? ((int64_t)n / 2 + 31) / 32 : ((int64_t)n + 63) / 64;
+    return slabs * kt * 4096;
+}
+
+hipError_t launch_pack(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu, uint8_t *out, hipStream_t stream) {
+    const int kt = (k + 63) / 64;
+    const int64_t chunks = packed_bytes(k, n, glu) / 16;
+    if (chunks == 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_kernel, dim3(grid_for(chunks)), dim3(256), 0, stream, w, wl, ldw, k, n, glu ? 1 : 0, kt,
+                       chunks, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t columns, const void *scale,
                              int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out,

@@ -26,7 +26,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 enum WType { W_INT8 = 0, W_FP8 = 1 };
-enum WLayout { W_KN = 0, W_NK = 1 };
+enum WLayout { W_KN = 0, W_NK = 1, W_PACKED = 2 };
 enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_SILU_GLU = 2, EPI_SITU_GLU = 3 };
 enum OutT { OUT_BF16 = 0, OUT_F32 = 1 };
 

@@ -24,6 +24,7 @@ struct GemmArgs {
     int glu_half;           // h for GLU epilogues
     int scale_per_col;
     int a_vec, w_vec, c_vec; // 16-byte loads of A, wide loads of W, wide stores of C allowed
+    int kt;                 // K steps of 64 (the packed layout's K extent)
     int tiles_m, tiles_n;   // set by the launcher
 };
 
@@ -34,6 +35,18 @@ int choose_tile(int M, int N_out, bool glu);
 // loads (alignment), K is a positive multiple of 64, and there are at least 4 weight columns (per
 // GLU half) with a [K, N] weight's column count a multiple of 4.
 hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
+
+// The weight-direct kernels (sq8_wdirect_inst.hip): [N, K] or packed weights, K a multiple of 64,
+// A aligned for 16-byte loads. `tile`: WD_256 (256 rows) or WD_128 (128 rows), 256 columns.
+enum WdTile { WD_256 = 0, WD_128 = 1 };
+hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
+
+// Bytes of the packed layout of a weight with k rows of K and n columns (GLU: n = 2h, packed in
+// pairs of 32-column blocks of the two halves).
+int64_t packed_bytes(int k, int n, bool glu);
+// Writes the packed layout of codes `w` (layout W_KN or W_NK, leading dimension ldw) into `out`.
+hipError_t launch_pack(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu, uint8_t *out,
+                       hipStream_t stream);
 
 // Auxiliary kernels (sq8_aux.hip).
 hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t columns, const void *scale,

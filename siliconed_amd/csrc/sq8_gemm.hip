@@ -9,6 +9,12 @@ hipError_t launch_fast_0_1(const GemmArgs &p, int tile, int epi, int out, hipStr
 hipError_t launch_fast_1_0(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 hipError_t launch_fast_1_1(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 hipError_t launch_general(const GemmArgs &p, int wt, int wl, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_0(const GemmArgs &p, int tile, int wl, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_1(const GemmArgs &p, int tile, int wl, int epi, int out, hipStream_t stream);
+
+hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream) {
+    return wt == W_INT8 ? launch_wdirect_0(p, tile, wl, epi, out, stream) : launch_wdirect_1(p, tile, wl, epi, out, stream);
+}
 
 int choose_tile(int M, int N_out, bool glu) {
     // Tiles of 256 × 256 while they fill the 256 CUs at least 3/4 of the way; 128 × 128 below.

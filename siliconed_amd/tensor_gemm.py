@@ -27,6 +27,18 @@ _EPILOGUES = {
 _LAYOUTS = {"kn": abi.KN, "nk": abi.NK}
 
 
+class PackedWeight:
+    """A weight's codes staged in the packed layout (sq8_pack_weight): `k` × `n` codes of
+    `w_dtype`, paired for a GLU epilogue when `glu`. The scales stay where they were."""
+
+    def __init__(self, data: torch.Tensor, k: int, n: int, glu: bool, w_dtype: int):
+        self.data, self.k, self.n, self.glu, self.w_dtype = data, k, n, glu, w_dtype
+
+    @property
+    def layout(self) -> int:
+        return abi.PACKED_GLU if self.glu else abi.PACKED
+
+
 def _epilogue(name) -> int:
     if name not in _EPILOGUES:
         raise ValueError(f"unknown epilogue {name!r}")
@@ -166,6 +178,25 @@ class TensorGEMM:
         abi.check(st, "sq8_linear")
         return 0.0 if settled else secs.value
 
+    # ---- staging -----------------------------------------------------------------------------
+
+    def pack(self, w: torch.Tensor, *, layout: str = "nk", glu: bool = False,
+             fp8: Optional[bool] = None) -> PackedWeight:
+        """Stages codes W ([n, k] for "nk", [k, n] for "kn") into the packed layout, once
+        (Artifact.stageInt8's place, Sources/Siliconed/Artifact.swift:755-774)."""
+        lay = _LAYOUTS[layout]
+        wd = _wdtype(w, fp8)
+        if w.dim() != 2:
+            raise ValueError("w must be 2-D")
+        n, k = (w.shape[0], w.shape[1]) if lay == abi.NK else (w.shape[1], w.shape[0])
+        if glu and n % 2:
+            raise ValueError("a GLU weight has an even number of columns")
+        size = abi.load().sq8_packed_bytes(k, n, int(glu))
+        out = torch.empty(max(size, 1), dtype=torch.uint8, device=w.device)
+        st = abi.load().sq8_pack_weight(self._h, _dev(w, "w"), lay, _row_major(w, "w"), k, n, int(glu), out.data_ptr())
+        abi.check(st, "sq8_pack_weight")
+        return PackedWeight(out, k, n, glu, wd)
+
     # ---- tensor-level operations ---------------------------------------------------------------
 
     def product(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
@@ -174,15 +205,23 @@ class TensorGEMM:
                 timed: bool = False):
         """y = act(s ⊙ (x · Wᵀ) + b) for x [m, k] and W [n, k] (`layout="nk"`, nn.Linear) or
         [k, n] (`"kn"`, the map's). Returns y (and the GPU seconds when `timed`)."""
-        lay = _LAYOUTS[layout]
-        wd = _wdtype(w, fp8)
         epi = _epilogue(epilogue)
-        if w.dim() != 2:
-            raise ValueError("w must be 2-D")
         m, k = x.shape
-        n = w.shape[0] if lay == abi.NK else w.shape[1]
-        if (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
-            raise ValueError(f"x [{m}, {k}] and w {tuple(w.shape)} ({layout}) disagree on K")
+        if isinstance(w, PackedWeight):
+            lay, wd, n, ldw, wptr = w.layout, w.w_dtype, w.n, w.k, _dev(w.data, "w")
+            if w.k != k:
+                raise ValueError(f"x [{m}, {k}] and the packed weight disagree on K ({w.k})")
+            if w.glu != (epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU)):
+                raise ValueError("a weight packed for a GLU epilogue serves GLU epilogues only, and only those")
+        else:
+            lay = _LAYOUTS[layout]
+            wd = _wdtype(w, fp8)
+            if w.dim() != 2:
+                raise ValueError("w must be 2-D")
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            if (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
+                raise ValueError(f"x [{m}, {k}] and w {tuple(w.shape)} ({layout}) disagree on K")
+            ldw, wptr = _row_major(w, "w"), _dev(w, "w")
         glu = epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU)
         if glu and n % 2:
             raise ValueError("a GLU epilogue needs an even number of weight columns")
@@ -199,7 +238,7 @@ class TensorGEMM:
         secs = ctypes.c_double(0.0)
         st = abi.load().sq8_linear(
             self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
-            _dev(w, "w"), wd, lay, _row_major(w, "w"),
+            wptr, wd, lay, ldw,
             _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
             None if bias is None else _dev(bias, "bias"), epi,
             _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
@@ -212,10 +251,14 @@ class TensorGEMM:
                     out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None):
         """Fused QKV: W of 3·d output channels; returns (q, k, v), each [m, d] (head_dim 0) or
         [d/head_dim, m, head_dim]."""
-        lay = _LAYOUTS[layout]
-        wd = _wdtype(w, fp8)
         m, k = x.shape
-        n = w.shape[0] if lay == abi.NK else w.shape[1]
+        if isinstance(w, PackedWeight):
+            lay, wd, n, ldw, wptr = w.layout, w.w_dtype, w.n, w.k, _dev(w.data, "w")
+        else:
+            lay = _LAYOUTS[layout]
+            wd = _wdtype(w, fp8)
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            ldw, wptr = _row_major(w, "w"), _dev(w, "w")
         if n % 3:
             raise ValueError("a fused QKV weight has 3·d output channels")
         d = n // 3
@@ -224,7 +267,7 @@ class TensorGEMM:
         per_col = scale.numel() != 1
         st = abi.load().sq8_linear_qkv(
             self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
-            _dev(w, "w"), wd, lay, _row_major(w, "w"),
+            wptr, wd, lay, ldw,
             _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
             None if bias is None else _dev(bias, "bias"),
             q.data_ptr(), kk.data_ptr(), v.data_ptr(), _cdtype(out_dtype), d, head_dim, m, k, d, None)
@@ -286,6 +329,10 @@ def linear(x, w, scale, **kw):
 
 def linear_qkv(x, w, scale, **kw):
     return context(x.device.index).product_qkv(x, w, scale, **kw)
+
+
+def pack(w, **kw):
+    return context(w.device.index).pack(w, **kw)
 
 
 def dequantize(codes, scale=None, **kw):

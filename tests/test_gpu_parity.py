@@ -274,3 +274,67 @@ def test_baseline_shapes_sampled_rows(gemm, orc, case):
     for layout in ("kn", "nk"):
         got = run(gemm, x, q, s, b, fp8, layout, epi, torch.bfloat16)
         judge(orc, got, x, q, fp8, s, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+# ---- the packed layout (sq8_pack_weight) ------------------------------------------------------------
+
+PACKED_SHAPES = [(256, 3072, 3072), (150, 768, 96), (70, 10240, 72), (65, 448, 130), (300, 1024, 1000), (1, 64, 8)]
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+@pytest.mark.parametrize("shape", PACKED_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_packed_product(gemm, orc, shape, fp8):
+    m, k, n = shape
+    x, q, s, b = problem(orc, m, k, n, fp8, seed=500 + n)
+    xt, st, bt = bf16_dev(x), dev(s), dev(b)
+    wnk, wkn = weight_tensor(q, fp8, "nk"), weight_tensor(q, fp8, "kn")
+    pk_nk = gemm.pack(wnk, layout="nk", fp8=fp8 or None)
+    pk_kn = gemm.pack(wkn, layout="kn", fp8=fp8 or None)
+    assert torch.equal(pk_nk.data, pk_kn.data)  # the same codes, the same packed bytes
+    for out in (torch.float32, torch.bfloat16):
+        y = gemm.product(xt, pk_kn, st, bias=bt, out_dtype=out)
+        direct = gemm.product(xt, wnk, st, layout="nk", bias=bt, out_dtype=out)
+        torch.cuda.synchronize()
+        assert torch.equal(y, direct)  # one kernel, one K order: the same bits
+        judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, "none", out)
+
+
+@pytest.mark.parametrize("epi", ["gelu", "silu", "situ"])
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+def test_packed_epilogues(gemm, orc, epi, fp8):
+    for m, k, n in [(256, 1024, 768), (65, 448, 130), (512, 3072, 6144)]:
+        x, q, s, b = problem(orc, m, k, n, fp8, seed=9 + n)
+        glu = epi in ("silu", "situ")
+        pk = gemm.pack(weight_tensor(q, fp8, "kn"), layout="kn", glu=glu, fp8=fp8 or None)
+        name = {"gelu": "gelu_tanh", "silu": "silu_glu", "situ": "situ_glu"}[epi]
+        for out in (torch.float32, torch.bfloat16):
+            y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue=name, out_dtype=out)
+            torch.cuda.synchronize()
+            judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, epi, out)
+
+
+def test_packed_glu_weight_refuses_plain_epilogue(gemm, orc):
+    x, q, s, b = problem(orc, 64, 256, 128, False, seed=3)
+    pk = gemm.pack(weight_tensor(q, False, "nk"), layout="nk", glu=True)
+    with pytest.raises(ValueError):
+        gemm.product(bf16_dev(x), pk, dev(s))
+    from siliconed_amd import _abi as abi
+    assert abi.load().sq8_packed_bytes(100, 130, 0) == 2 * 3 * 4096
+    assert abi.load().sq8_packed_bytes(100, 130, 1) == 3 * 2 * 4096
+    assert abi.load().sq8_packed_bytes(64, 3, 1) == -1
+
+
+@pytest.mark.parametrize("case", ["c1_up_gelu", "c1_down", "c2_qkv", "c3_gate_up_fp8"])
+def test_packed_baseline_shapes(gemm, orc, case):
+    m, k, n, fp8, epi = {
+        "c1_up_gelu": (4096, 3072, 12288, False, "gelu"),
+        "c1_down": (4096, 12288, 3072, False, "none"),
+        "c2_qkv": (4608, 3072, 9216, False, "none"),
+        "c3_gate_up_fp8": (4096, 3840, 20480, True, "silu"),
+    }[case]
+    x, q, s, b = problem(orc, m, k, n, fp8, seed=2000 + k)
+    pk = gemm.pack(weight_tensor(q, fp8, "kn"), layout="kn", glu=epi == "silu", fp8=fp8 or None)
+    name = {"gelu": "gelu_tanh", "silu": "silu_glu", "none": None}[epi]
+    y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue=name, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
