@@ -26,8 +26,10 @@ SOURCES = [
     ("sq8_gemm_inst.hip", "sq8_gemm_i8_nk", ["-DSQ8_WT=0", "-DSQ8_WL=1"]),
     ("sq8_gemm_inst.hip", "sq8_gemm_f8_kn", ["-DSQ8_WT=1", "-DSQ8_WL=0"]),
     ("sq8_gemm_inst.hip", "sq8_gemm_f8_nk", ["-DSQ8_WT=1", "-DSQ8_WL=1"]),
-    ("sq8_wdirect_inst.hip", "sq8_wdirect_i8", ["-DSQ8_WT=0"]),
-    ("sq8_wdirect_inst.hip", "sq8_wdirect_f8", ["-DSQ8_WT=1"]),
+    ("sq8_wdirect_inst.hip", "sq8_wdirect_i8_nk", ["-DSQ8_WT=0", "-DSQ8_WL=1"]),
+    ("sq8_wdirect_inst.hip", "sq8_wdirect_i8_packed", ["-DSQ8_WT=0", "-DSQ8_WL=2"]),
+    ("sq8_wdirect_inst.hip", "sq8_wdirect_f8_nk", ["-DSQ8_WT=1", "-DSQ8_WL=1"]),
+    ("sq8_wdirect_inst.hip", "sq8_wdirect_f8_packed", ["-DSQ8_WT=1", "-DSQ8_WL=2"]),
     ("sq8_aux.hip", "sq8_aux", []),
     ("sq8_api.hip", "sq8_api", []),
 ]

@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <new>
@@ -152,6 +153,14 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (q.head_dim > 0) cv = cv && (q.head_dim % 4) == 0;
     else cv = cv && (q.ldc % 4) == 0;
     p.c_vec = cv;
+    // 16-byte stores: 8 bf16 / 4 fp32 columns that never straddle a split or a head.
+    const int per16 = (int)(16 / esz);
+    bool cv16 = true;
+    for (int i = 0; i < (q.split > 0 ? 3 : 1); ++i) cv16 = cv16 && aligned(q.c[i], 16);
+    if (q.split > 0) cv16 = cv16 && (q.split % per16) == 0;
+    if (q.head_dim > 0) cv16 = cv16 && (q.head_dim % per16) == 0;
+    else cv16 = cv16 && (q.ldc % per16) == 0;
+    p.c_vec16 = cv16;
 
     const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
@@ -163,8 +172,9 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
         const int wl = is_packed(q.w_layout) ? sq8::W_PACKED : sq8::W_NK;
-        const long tiles256 = (long)((q.m + 255) / 256) * ((q.n + 255) / 256);
-        const int tile = tiles256 >= 160 ? sq8::WD_256 : sq8::WD_128;
+        int tile = sq8::WD_128;
+        const char *force = getenv("SQ8_TILE");  // measurement knob: "256" or "128"
+        if (force && strcmp(force, "256") == 0) tile = sq8::WD_256;
         e = sq8::launch_wdirect(p, tile, wt, wl, q.epilogue, out, ctx->stream);
     } else {
         const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;

@@ -101,15 +101,21 @@ __device__ __forceinline__ float tanh_fast(float y) {
     return copysignf(t, y);
 }
 
+// GELU-tanh: ½·x·(1 + tanh(u)) with u = √(2/π)·(x + 0.044715·x³), computed as its identical form
+// x·σ(2u) = x / (1 + e^{−2u}) — one exponential and one reciprocal; e^{−2u} overflowing gives
+// x/∞ = −0 for large negative x, as the tanh form's ½·x·0.
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float c = 0.7978845608028654f;  // √(2/π)
-    float u = c * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanh_fast(u));
+    const float k = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // −2·√(2/π)·log2(e)
+    const float x2 = x * x;
+    const float q = x * __builtin_fmaf(0.044715f, x2, 1.0f);
+    const float e = __builtin_amdgcn_exp2f(q * k);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // silu(g)·u = g/(1 + e^{−g})·u; e^{−g} overflowing gives −0·u as the reference's.
 __device__ __forceinline__ float silu_glu(float g, float u) {
-    return __fdividef(g, 1.0f + __expf(-g)) * u;
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 // tanh with a small relative error everywhere: below |y| = 1/4 the odd Taylor polynomial to y⁹

@@ -24,6 +24,7 @@ struct GemmArgs {
     int glu_half;           // h for GLU epilogues
     int scale_per_col;
     int a_vec, w_vec, c_vec; // 16-byte loads of A, wide loads of W, wide stores of C allowed
+    int c_vec16;            // 16-byte stores of C allowed (aligned base, stride, split and head size)
     int kt;                 // K steps of 64 (the packed layout's K extent)
     int tiles_m, tiles_n;   // set by the launcher
 };
@@ -37,7 +38,8 @@ int choose_tile(int M, int N_out, bool glu);
 hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
 
 // The weight-direct kernels (sq8_wdirect_inst.hip): [N, K] or packed weights, K a multiple of 64,
-// A aligned for 16-byte loads. `tile`: WD_256 (256 rows) or WD_128 (128 rows), 256 columns.
+// A aligned for 16-byte loads. `tile`: WD_256 (256 × 256, one workgroup per CU) or WD_128 (128 × 256,
+// two workgroups per CU).
 enum WdTile { WD_256 = 0, WD_128 = 1 };
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
 

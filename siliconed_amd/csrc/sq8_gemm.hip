@@ -9,11 +9,14 @@ hipError_t launch_fast_0_1(const GemmArgs &p, int tile, int epi, int out, hipStr
 hipError_t launch_fast_1_0(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 hipError_t launch_fast_1_1(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 hipError_t launch_general(const GemmArgs &p, int wt, int wl, int epi, int out, hipStream_t stream);
-hipError_t launch_wdirect_0(const GemmArgs &p, int tile, int wl, int epi, int out, hipStream_t stream);
-hipError_t launch_wdirect_1(const GemmArgs &p, int tile, int wl, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_0_1(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_0_2(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_1_1(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
+hipError_t launch_wdirect_1_2(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream) {
-    return wt == W_INT8 ? launch_wdirect_0(p, tile, wl, epi, out, stream) : launch_wdirect_1(p, tile, wl, epi, out, stream);
+    if (wt == W_INT8) return wl == W_NK ? launch_wdirect_0_1(p, tile, epi, out, stream) : launch_wdirect_0_2(p, tile, epi, out, stream);
+    return wl == W_NK ? launch_wdirect_1_1(p, tile, epi, out, stream) : launch_wdirect_1_2(p, tile, epi, out, stream);
 }
 
 int choose_tile(int M, int N_out, bool glu) {

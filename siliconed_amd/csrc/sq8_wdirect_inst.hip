@@ -1,9 +1,9 @@
-// sq8_wdirect_inst.hip — instantiates the weight-direct kernels for one weight type (SQ8_WT),
-// compiled once per type so the two sets build in parallel.
+// sq8_wdirect_inst.hip — instantiates the weight-direct kernels for one weight type (SQ8_WT) and
+// layout (SQ8_WL: 1 [N, K], 2 packed), compiled once per pair so the sets build in parallel.
 #include "sq8_wdirect_kernel.h"
 
-#if !defined(SQ8_WT)
-#error "compile with -DSQ8_WT=<0 int8 | 1 fp8>"
+#if !defined(SQ8_WT) || !defined(SQ8_WL)
+#error "compile with -DSQ8_WT=<0 int8 | 1 fp8> -DSQ8_WL=<1 [N,K] | 2 packed>"
 #endif
 
 #define SQ8_CAT2(a, b) a##b
@@ -11,12 +11,10 @@
 
 namespace sq8 {
 
-hipError_t SQ8_CAT(launch_wdirect_, SQ8_WT)(const GemmArgs &p, int tile, int wl, int epi, int out,
-                                            hipStream_t stream) {
-    if (tile == WD_256 && wl == W_NK) return wd::dispatch_wd<256, 4, SQ8_WT, W_NK>(p, epi, out, stream);
-    if (tile == WD_256 && wl == W_PACKED) return wd::dispatch_wd<256, 4, SQ8_WT, W_PACKED>(p, epi, out, stream);
-    if (tile == WD_128 && wl == W_NK) return wd::dispatch_wd<128, 4, SQ8_WT, W_NK>(p, epi, out, stream);
-    if (tile == WD_128 && wl == W_PACKED) return wd::dispatch_wd<128, 4, SQ8_WT, W_PACKED>(p, epi, out, stream);
+hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const GemmArgs &p, int tile, int epi, int out,
+                                                                       hipStream_t stream) {
+    if (tile == WD_256) return wd::dispatch_wd<256, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     return hipErrorInvalidValue;
 }
 

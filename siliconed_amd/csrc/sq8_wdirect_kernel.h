@@ -1,6 +1,6 @@
 // sq8_wdirect_kernel.h — the weight-direct gfx950 GEMM: each wave owns a 64-column slab of the
-// weight and streams its 8-bit codes from HBM straight into registers, widening them to bf16 there
-// while the previous K step's MFMAs run; only the activation tile goes through LDS.
+// weight and streams its 8-bit codes from HBM straight into registers, widening them to bf16 there;
+// only the activation tile goes through LDS.
 //
 // Arithmetic as the other kernels (Sources/Siliconed/TensorGEMM.swift:124-135, :173-179):
 // C = act(s ⊙ (A·q) + b), exact bf16 × code products, fp32 sums, scale after the sum, bias after
@@ -18,17 +18,24 @@
 // Activation: a 2-stage LDS ring of [BM][64] bf16 tiles filled by direct global→LDS loads
 // (global_load_lds_dwordx4: each wave writes 1 KB = 8 rows per load, no VGPR, no ds_write), rows
 // of 128 bytes whose 16-byte chunks are XOR-swizzled (chunk ^ ((r ^ r>>3) & 7)) so the fragment
-// reads of 16 consecutive rows hit distinct banks.
+// reads of 16 consecutive rows hit distinct banks. Fragments of sub-step ks+1 are read while the
+// MFMAs of ks run.
 //
-// Pipeline per K step t (all loads issued ahead, the waits explicit):
-//   issue A(t+1) → LDS stage (t+1)&1, issue W(t+2) → raw[t&1]        (clamped past the end)
-//   wait W(t+1)                                                        vmcnt(A loads + 4)
-//   MFMAs of step t  ∥  widen raw[(t+1)&1] → fragments of step t+1
-//   wait A(t+1), barrier                                                vmcnt(4)
+// Two pipelines, by occupancy:
+//   OCC = 1 (one workgroup per CU): the codes of step t+1 are widened between the MFMAs of step t;
+//     fragments double-buffered.
+//   OCC = 2 (two workgroups per CU, ≤ 256 registers a wave): the codes of step t are widened at the
+//     step's start — the other workgroup's MFMAs cover it — into one fragment buffer.
+// Per step t, the loads issued ahead and the waits explicit (vmcnt counts in issue order):
+//   [widen W(t)]  issue A(t+1) → LDS stage (t+1)&1, W(t+2) → raw[t&1]  MFMAs of t  wait vmcnt(4)
+//   (A(t+1) and W(t+1) landed)  barrier (no fence: the W prefetch stays in flight)
 //
 // Weight layouts: [N, K] (nn.Linear: row-strided 16-byte loads) or the packed layout of
 // sq8_pack_weight — per 64-column slab, per K step, per load j, per lane, 16 bytes — in which each
 // wave load is one contiguous kilobyte.
+//
+// Epilogue: scale, bias, activation in registers; each 32 × 32 block goes through a wave-private
+// LDS region and leaves as 16-byte row segments (coalesced rows instead of 8-byte pieces of 32).
 #pragma once
 
 #include "sq8_gemm_kernel.h"
@@ -50,13 +57,12 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroup barrier ordering LDS only: the release/acquire fences are restricted to the local
-// address space, so loads still in flight to registers (the weight prefetch) are not drained.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// The K-loop's workgroup barrier: s_barrier, and a compiler barrier for memory operations — no
+// fence. Across it, the LDS is written only by the direct global→LDS loads, which each wave has
+// waited for (vmcnt) before arriving, and read only by fragment loads whose results the MFMAs
+// already consumed; a fence would add vmcnt(0) for those LDS-bound loads, draining the weight
+// prefetch the vmcnt counter holds behind them.
+__device__ __forceinline__ void step_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // 8 codes (two dwords) → one MFMA operand of 8 bf16, exactly.
 template <int WT>
@@ -67,12 +73,13 @@ __device__ __forceinline__ bf16x8 widen8(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(bf16x8, u32x4{o0, o1, o2, o3});
 }
 
-// Byte offset of the 16 bytes lane `lane`, load j (block j>>1, half j&1) of K step 0 reads for
-// virtual 64-column slab `slab`, or −1 when the column is past the edge (zero-filled instead).
+// Byte offset (K step 0) of the 16 bytes lane `lane`, load j (block j>>1, half j&1) reads for
+// virtual 64-column slab `slab`. Past the edge of an [N, K] weight: the last column of the same half
+// (its results are never stored).
 template <int WL, bool GLU>
-__device__ __forceinline__ int64_t w_offset(const GemmArgs &p, int slab, int j, int lane) {
+__device__ __forceinline__ uint32_t w_offset(const GemmArgs &p, int slab, int j, int lane) {
     if constexpr (WL == W_PACKED) {
-        return ((int64_t)slab * p.kt * 4 + j) * 1024 + lane * 16;
+        return (uint32_t)(((int64_t)slab * p.kt * 4 + j) * 1024 + lane * 16);
     } else {
         const int b = j >> 1, c = j & 1, h = lane >> 5, nl = lane & 31;
         int n;
@@ -83,22 +90,122 @@ __device__ __forceinline__ int64_t w_offset(const GemmArgs &p, int slab, int j, 
             n = slab * 64 + b * 32 + nl;
             n = n < p.N ? n : p.N - 1;
         }
-        return (int64_t)n * p.ldw + 32 * h + 16 * c;
+        return (uint32_t)((int64_t)n * p.ldw + 32 * h + 16 * c);
     }
 }
 
-template <int BM, int NW, int WT, int WL, int EPI, int OUT>
-__global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(1, 1)))
+// Byte offset in output tensor `which` of row m, column col (the QKV split and head layout).
+__device__ __forceinline__ int64_t out_index(const GemmArgs &p, int m, int col, int &which) {
+    int cc = col;
+    which = 0;
+    if (p.split > 0) {
+        which = col / p.split;
+        cc = col - which * p.split;
+    }
+    return p.head_dim > 0 ? ((int64_t)(cc / p.head_dim) * p.M + m) * p.head_dim + cc % p.head_dim
+                          : (int64_t)m * p.ldc + cc;
+}
+
+// Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
+// `x` (and `u`), written to the wave's LDS region as rows of 32 values, then stored as 16-byte row
+// segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const f32x16 &u, int col0, int m_first,
+                                            int n_out, uint8_t *region, int lane) {
+    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
+    constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
+    constexpr int PITCH = 32 * ESZ + 16;  // row bytes + 16: keeps 16-byte alignment, spreads banks
+    const int h = lane >> 5, r = lane & 31;
+    static_for<0, 4>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        const int c = 8 * g + 4 * h;  // first of this lane's 4 columns in the block
+        const int col = col0 + c;
+        float s1[4], b1[4] = {0, 0, 0, 0}, s2[4], b2[4] = {0, 0, 0, 0};
+        if (col + 4 <= n_out && p.scale_per_col) {
+            const f32x4 sv = *reinterpret_cast<const f32x4 *>(p.scale + col);
+            s1[0] = sv[0]; s1[1] = sv[1]; s1[2] = sv[2]; s1[3] = sv[3];
+            if (GLU) {
+                const f32x4 sw = *reinterpret_cast<const f32x4 *>(p.scale + col + p.glu_half);
+                s2[0] = sw[0]; s2[1] = sw[1]; s2[2] = sw[2]; s2[3] = sw[3];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int cc = min(col + e, n_out - 1);
+                s1[e] = p.scale_per_col ? p.scale[cc] : p.scale[0];
+                s2[e] = p.scale_per_col ? p.scale[cc + (GLU ? p.glu_half : 0)] : p.scale[0];
+            }
+        }
+        if (p.bias) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int cc = min(col + e, n_out - 1);
+                b1[e] = p.bias[cc];
+                b2[e] = GLU ? p.bias[cc + p.glu_half] : 0.0f;
+            }
+        }
+        float y[4];
+        static_for<0, 4>([&](auto ec) {
+            constexpr int e = decltype(ec)::value;
+            float v = __fmul_rn(x[4 * g + e], s1[e]);
+            if (p.bias) v = __fadd_rn(v, b1[e]);
+            if constexpr (EPI == EPI_GELU) {
+                v = gelu_tanh(v);
+            } else if constexpr (GLU) {
+                float w = __fmul_rn(u[4 * g + e], s2[e]);
+                if (p.bias) w = __fadd_rn(w, b2[e]);
+                v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
+            }
+            y[e] = v;
+        });
+        uint8_t *dst = region + r * PITCH + c * ESZ;
+        if constexpr (OUT == OUT_BF16)
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
+        else
+            *reinterpret_cast<f32x4 *>(dst) = f32x4{y[0], y[1], y[2], y[3]};
+    });
+    // Read back as 16-byte row segments: CPR chunks per row, 64/CPR rows per pass. LDS operations
+    // of one wave complete in order, so the wave reads back what it just wrote.
+    constexpr int CPR = 32 * ESZ / 16;
+    constexpr int ROWS = 64 / CPR;
+    constexpr int PER = 16 / ESZ;  // values per chunk
+    static_for<0, 32 / ROWS>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const int row = lane / CPR + ROWS * i, chunk = lane % CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(region + row * PITCH + chunk * 16);
+        const int m = m_first + row;
+        const int col = col0 + chunk * PER;
+        if (m < p.M && col < n_out) {
+            int which;
+            const int64_t off = out_index(p, m, col, which);
+            if (col + PER <= n_out && p.c_vec16) {
+                *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(p.c[which]) + off * ESZ) = v;
+            } else {
+                const uint8_t *bytes = reinterpret_cast<const uint8_t *>(&v);
+                for (int e = 0; e < PER && col + e < n_out; ++e) {
+                    int we;
+                    const int64_t oe = out_index(p, m, col + e, we);
+                    uint8_t *oo = reinterpret_cast<uint8_t *>(p.c[we]) + oe * ESZ;
+                    for (int q = 0; q < ESZ; ++q) oo[q] = bytes[e * ESZ + q];
+                }
+            }
+        }
+    });
+}
+
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT>
+__global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
 gemm_wd_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int FM = BM / 32;                      // 32-row blocks per wave
     constexpr int SA = BM * 128;                     // bytes per A stage
     constexpr int A_BLOCKS = BM / 8;                 // 1 KB (8-row) blocks per A stage
-    constexpr int A_PER_WAVE = (A_BLOCKS + NW - 1) / NW;
-    constexpr bool A_EVEN = A_BLOCKS % NW == 0;
+    constexpr int A_PER_WAVE = A_BLOCKS / NW;
     // Every wave issues the same number of activation loads, so one vmcnt value fits them all.
-    static_assert(A_EVEN, "the activation blocks split evenly over the waves");
+    static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
     static_assert(A_PER_WAVE + 4 < 64, "vmcnt budget");
+    constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
+    static_assert(NW * REGION <= 2 * SA, "the epilogue regions fit in the A stages");
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SA];
 
@@ -116,7 +223,7 @@ gemm_wd_kernel(const GemmArgs p) {
     uint32_t a_goff[A_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < A_PER_WAVE; ++i) {
-        const int b = min(wave + NW * i, A_BLOCKS - 1);
+        const int b = wave + NW * i;
         const int r = 8 * b + (lane >> 3);
         const int lc = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
         const int row = min(m0 + r, p.M - 1);
@@ -124,32 +231,30 @@ gemm_wd_kernel(const GemmArgs p) {
     }
     auto issue_a = [&](int t, auto stage) {
         constexpr int S = decltype(stage)::value;
-        const uint32_t k_bytes = (uint32_t)min(t, KT - 1) * (BK * 2);
+        const kern::gbytes base = Ag + (uint32_t)min(t, KT - 1) * (BK * 2);
 #pragma unroll
-        for (int i = 0; i < A_PER_WAVE; ++i) {
-            if (A_EVEN || wave + NW * i < A_BLOCKS) {
-                __builtin_amdgcn_global_load_lds((glb_ptr)(Ag + a_goff[i] + k_bytes),
-                                                 (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024), 16, 0, 0);
-            }
-        }
+        for (int i = 0; i < A_PER_WAVE; ++i)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024),
+                                             16, 0, 0);
     };
 
     // ---- weight loads: 4 × 16 bytes per lane per K step --------------------------------------------
-    int64_t w_off[4];
+    uint32_t w_off[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, j, lane);
-    const int64_t w_step = WL == W_PACKED ? 4096 : BK;
+    const uint32_t w_step = WL == W_PACKED ? 4096 : BK;
     u32x4 raw[2][4];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
-        const int64_t k_off = (int64_t)min(t, KT - 1) * w_step;
+        const kern::gbytes base = Wg + (uint32_t)min(t, KT - 1) * w_step;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) raw[B][j] = *(const __attribute__((address_space(1))) u32x4 *)(Wg + w_off[j] + k_off);
+        for (int j = 0; j < 4; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
     };
 
     // ---- fragments -----------------------------------------------------------------------------------
-    bf16x8 wf[2][2][4];  // [buffer][block][ks]
-    auto widen_w = [&](auto src, auto dst) {
+    constexpr int WF = OCC == 1 ? 2 : 1;  // fragment buffers
+    bf16x8 wf[WF][2][4];                  // [buffer][block][ks]
+    auto widen_all = [&](auto src, auto dst) {
         constexpr int S = decltype(src)::value, D = decltype(dst)::value;
         static_for<0, 2>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
@@ -178,22 +283,27 @@ gemm_wd_kernel(const GemmArgs p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[b][bm][r] = 0.0f;
 
-    // One K step: the MFMAs on stage S with fragments F, the widening of raw[R] into fragments 1−F
-    // interleaved with them.
-    auto step = [&](auto stage, auto frag, auto rawbuf) {
+    // The MFMAs of one step on stage S with fragments F; OCC = 1 widens raw[R] into fragments 1−F
+    // between them. Activation fragments of sub-step ks+1 are read before the MFMAs of ks.
+    auto mfmas = [&](auto stage, auto frag, auto rawbuf) {
         constexpr int S = decltype(stage)::value, F = decltype(frag)::value, R = decltype(rawbuf)::value;
-        static_for<0, 4>([&](auto kc) {
-            constexpr int ks = decltype(kc)::value;
-            bf16x8 xf[FM];
+        bf16x8 xf[2][FM];
+        auto read_x = [&](auto kc, auto bufc) {
+            constexpr int ks = decltype(kc)::value, B = decltype(bufc)::value;
             static_for<0, FM>([&](auto bmc) {
                 constexpr int bm = decltype(bmc)::value;
-                xf[bm] = kern::lds_load_frag(lds + S * SA + 32 * 128 * bm, xo[bm & 1][ks]);
+                xf[B][bm] = kern::lds_load_frag(lds + S * SA + 32 * 128 * bm, xo[bm & 1][ks]);
             });
-            // Widen the next step's block (ks & 1), half (ks >> 1) while these MFMAs run.
-            {
+        };
+        read_x(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+        static_for<0, 4>([&](auto kc) {
+            constexpr int ks = decltype(kc)::value;
+            if constexpr (ks < 3) read_x(std::integral_constant<int, ks + 1>{}, std::integral_constant<int, (ks + 1) & 1>{});
+            if constexpr (OCC == 1) {
+                // Widen the next step's block ks >> 1, sub-steps 2(ks & 1) and 2(ks & 1) + 1.
                 constexpr int b = ks >> 1;
                 static_for<0, 2>([&](auto qc) {
-                    constexpr int q = 2 * (ks & 1) + decltype(qc)::value;  // next-step ks index
+                    constexpr int q = 2 * (ks & 1) + decltype(qc)::value;
                     const u32x4 &r = raw[R][2 * b + (q >> 1)];
                     wf[1 - F][b][q] = widen8<WT>(r[2 * (q & 1)], r[2 * (q & 1) + 1]);
                 });
@@ -202,7 +312,7 @@ gemm_wd_kernel(const GemmArgs p) {
                 constexpr int b = decltype(bc)::value;
                 static_for<0, FM>([&](auto bmc) {
                     constexpr int bm = decltype(bmc)::value;
-                    acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[F][b][ks], xf[bm], acc[b][bm], 0, 0, 0);
+                    acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[F][b][ks], xf[ks & 1][bm], acc[b][bm], 0, 0, 0);
                 });
             });
         });
@@ -210,60 +320,70 @@ gemm_wd_kernel(const GemmArgs p) {
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    constexpr int A_LOADS = A_PER_WAVE;  // activation loads each wave issues per step
 
-    // Prologue: A(0) → stage 0, W(0) → raw[0], W(1) → raw[1]; fragments of step 0.
+    // Prologue: A(0) → stage 0, W(0) → raw[0], W(1) → raw[1]; A(0) and W(0) landed.
     issue_a(0, I0{});
     issue_w(0, I0{});
     issue_w(1, I1{});
     wait_vmcnt<4>();
-    widen_w(I0{}, I0{});
-    lds_barrier();
+    if constexpr (OCC == 1) widen_all(I0{}, I0{});
+    step_barrier();
 
-    // Steps in pairs so every buffer index is a constant: step t uses stage t&1, fragments t&1,
-    // and widens raw[(t+1)&1]; W(t+2) goes to raw[t&1].
+    // One step t of parity P: stage P, W(t) in raw[P] (OCC 2 widens it here; OCC 1 widened it during
+    // step t−1 and widens W(t+1) from raw[1−P] now).
+    auto one_step = [&](int t, auto par) {
+        constexpr int P = decltype(par)::value;
+        if constexpr (OCC == 2) {
+            // Widen first and keep it first: the scheduler would otherwise sink the widening into the
+            // MFMAs and, the raw registers being read late, push the next loads to the step's end —
+            // or hoist it above the previous barrier.
+            __builtin_amdgcn_sched_barrier(0);
+            widen_all(std::integral_constant<int, P>{}, I0{});
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        issue_a(t + 1, std::integral_constant<int, 1 - P>{});
+        issue_w(t + 2, std::integral_constant<int, P>{});
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (OCC == 1) {
+            // W(t+1) must have landed before it is widened: the loads after it are this step's.
+            wait_vmcnt<A_PER_WAVE + 4>();
+            mfmas(std::integral_constant<int, P>{}, std::integral_constant<int, P>{}, std::integral_constant<int, 1 - P>{});
+        } else {
+            mfmas(std::integral_constant<int, P>{}, I0{}, I0{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<4>();
+        step_barrier();
+    };
     int t = 0;
     for (; t + 1 < KT; t += 2) {
-        issue_a(t + 1, I1{});
-        issue_w(t + 2, I0{});
-        wait_vmcnt<A_LOADS + 4>();
-        step(I0{}, I0{}, I1{});
-        wait_vmcnt<4>();
-        lds_barrier();
-        issue_a(t + 2, I0{});
-        issue_w(t + 3, I1{});
-        wait_vmcnt<A_LOADS + 4>();
-        step(I1{}, I1{}, I0{});
-        wait_vmcnt<4>();
-        lds_barrier();
+        one_step(t, I0{});
+        one_step(t + 1, I1{});
     }
-    if (t < KT) {  // odd KT: the last step on stage 0 (its widening works on a clamped copy)
-        issue_a(t + 1, I1{});
-        issue_w(t + 2, I0{});
-        wait_vmcnt<A_LOADS + 4>();
-        step(I0{}, I0{}, I1{});
-    }
+    if (t < KT) one_step(t, I0{});
+    // Every wave's last (clamped) activation load has landed before any wave writes its epilogue
+    // region over the stages.
     wait_vmcnt<0>();
+    step_barrier();
 
     // ---- epilogue ------------------------------------------------------------------------------
     // Lane l, register r of block (b, bm): row m0 + 32·bm + (l & 31), slab column
-    // 32·b + 8·(r >> 2) + 4·(l >> 5) + (r & 3).
+    // 32·b + 8·(r >> 2) + 4·(l >> 5) + (r & 3). The A stages are free: every wave passed the last
+    // barrier after its last fragment read and after its last load into them landed.
     const int n_out = GLU ? p.glu_half : p.N;
-    constexpr int NB = GLU ? 1 : 2;
-    static_for<0, NB>([&](auto bc) {
-        constexpr int b = decltype(bc)::value;
-        static_for<0, 4>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            const int nl = 8 * g + 4 * h;
-            const int col = GLU ? slab * 32 + nl : slab * 64 + b * 32 + nl;
-            if (col < n_out) {
-                kern::epilogue_store<FM, EPI, OUT, g>(p, acc[b], acc[GLU ? 1 : b], col, n_out, m0 + (lane & 31));
-            }
+    uint8_t *region = lds + wave * REGION;
+    static_for<0, FM>([&](auto bmc) {
+        constexpr int bm = decltype(bmc)::value;
+        static_for<0, GLU ? 1 : 2>([&](auto bc) {
+            constexpr int b = decltype(bc)::value;
+            const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
+            if (col0 < n_out)
+                store_block<EPI, OUT>(p, acc[b][bm], acc[GLU ? 1 : b][bm], col0, m0 + 32 * bm, n_out, region, lane);
         });
     });
 }
 
-template <int BM, int NW, int WT, int WL, int EPI, int OUT>
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT>
 hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
@@ -272,14 +392,14 @@ hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = (slabs + NW - 1) / NW;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, WT, WL, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int WT, int WL>
+template <int BM, int NW, int OCC, int WT, int WL>
 hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) {
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_wd<BM, NW, WT, WL, E, O>(p, stream);
+    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
