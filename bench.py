@@ -30,6 +30,9 @@ M, K, N = 4096, 3072, 12288
 SEEDS = {"x": 1, "w": 2, "scale": 3, "bias": 4}
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
+# HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a 512 MiB copy),
+# measured by the rocprofv3 --pmc runs in profiles/gemm_wd_kernel_c1_up_int8_packed_gelu.md, by weight layout.
+TRAFFIC_BYTES = {"packed": 483.3e6}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
 
@@ -104,6 +107,9 @@ def main() -> int:
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once from [K, N] by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="instead of the product, copy MIB MiB device→device --steps times (the known-size kernel "
+                         "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
@@ -114,6 +120,15 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        nbytes = args.copy_probe << 20
+        src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": nbytes, "launches": args.steps}), flush=True)
+        return 0
     x, q_kn, s, b = inputs()
     q = np.ascontiguousarray(q_kn.T) if args.layout == "nk" else q_kn
     xd = x.to(dev)
@@ -145,6 +160,7 @@ def main() -> int:
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # The events are recorded on torch's current stream, the stream the context launches on.
     kernel_ms = ev0.elapsed_time(ev1) / args.steps
     flops = 2.0 * M * N * K
     tflops = flops / (kernel_ms * 1e-3) / 1e12
@@ -172,7 +188,8 @@ def main() -> int:
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kernel_ms, 5),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": TRAFFIC_BYTES.get(args.layout),
                      "algorithmic_bytes": algo_bytes,
                      "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5)},
         "device": {"name": props.name, "cus": props.multi_processor_count},
