@@ -134,6 +134,10 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     p.c[0] = q.c[0];
     p.c[1] = q.c[1];
     p.c[2] = q.c[2];
+    if (q.split > 0) {
+        p.c_d1 = (int64_t)((uintptr_t)q.c[1] - (uintptr_t)q.c[0]);
+        p.c_d2 = (int64_t)((uintptr_t)q.c[2] - (uintptr_t)q.c[0]);
+    }
     p.ldc = q.ldc;
     p.split = q.split;
     p.head_dim = q.head_dim;
@@ -161,6 +165,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (q.head_dim > 0) cv16 = cv16 && (q.head_dim % per16) == 0;
     else cv16 = cv16 && (q.ldc % per16) == 0;
     p.c_vec16 = cv16;
+    p.sb_vec = aligned(p.scale, 16) && (!p.bias || aligned(p.bias, 16)) && (p.glu_half % 4) == 0;
 
     const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;

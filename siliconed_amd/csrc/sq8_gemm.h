@@ -17,6 +17,7 @@ struct GemmArgs {
     const float *scale;     // fp32 [N] (scale_per_col) or [1]
     const float *bias;      // fp32 [N] or null
     void *c[3];             // outputs; c[1], c[2] only with `split`
+    int64_t c_d1, c_d2;     // byte offsets of c[1], c[2] from c[0] (the device never indexes c[])
     int64_t ldc;
     int split;              // > 0: output columns [i·split, (i+1)·split) go to c[i]
     int head_dim;           // > 0: each output is [cols/head_dim, M, head_dim]
@@ -25,6 +26,7 @@ struct GemmArgs {
     int scale_per_col;
     int a_vec, w_vec, c_vec; // 16-byte loads of A, wide loads of W, wide stores of C allowed
     int c_vec16;            // 16-byte stores of C allowed (aligned base, stride, split and head size)
+    int sb_vec;             // 16-byte loads of 4 scales / biases allowed (aligned bases, GLU half % 4 == 0)
     int kt;                 // K steps of 64 (the packed layout's K extent)
     int tiles_m, tiles_n;   // set by the launcher
 };

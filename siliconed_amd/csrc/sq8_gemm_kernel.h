@@ -59,6 +59,14 @@ __device__ __forceinline__ T gld(gbytes base, uint32_t off) {
 // Workgroup → tile. The dispatcher hands workgroup i to XCD i mod 8; consecutive logical tiles
 // are given to one XCD, then ordered in groups of GROUP_M tile rows so an XCD's resident tiles
 // share A rows and W columns in its L2. A bijection on [0, tiles) whatever the dispatch order.
+// Base of output tensor `which` (0..2): c[0] plus a byte offset. Never p.c[which] (nor a select of
+// c[1] / c[2], which the compiler folds back into one): a run-time index into the argument struct
+// forces the whole struct into memory, a per-thread copy the compiler places in LDS.
+__device__ __forceinline__ uint8_t *out_base(const GemmArgs &p, int which) {
+    const int64_t d = (which == 1 ? p.c_d1 : 0) + (which == 2 ? p.c_d2 : 0);
+    return reinterpret_cast<uint8_t *>(p.c[0]) + d;
+}
+
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
     const int total = tiles_m * tiles_n;
     const int q = total >> 3, r = total & 7;
@@ -125,7 +133,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &p, const f32x16 (
         which = col / p.split;
         ccol = col - which * p.split;
     }
-    uint8_t *base = reinterpret_cast<uint8_t *>(p.c[which]);
+    uint8_t *base = out_base(p, which);
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
         const int m = m_first + bm * 32;

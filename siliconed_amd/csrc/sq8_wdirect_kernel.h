@@ -106,12 +106,46 @@ __device__ __forceinline__ int64_t out_index(const GemmArgs &p, int m, int col, 
                           : (int64_t)m * p.ldc + cc;
 }
 
+// Scales and biases of a lane's 16 columns of one 32-column block: group g holds columns
+// col0 + 8g + 4h + [0, 4) (h = lane ÷ 32), the layout of the MFMA output registers. `off`: where the
+// block's weight columns start relative to its output columns (the second half of a GLU weight).
+struct ColParams {
+    float s[4][4], b[4][4];
+};
+
+__device__ __forceinline__ void load_col_params(const GemmArgs &p, ColParams &cp, int col0, int off, int n_out,
+                                                int lane) {
+    const kern::gbytes S = (kern::gbytes)p.scale;
+    const kern::gbytes B = (kern::gbytes)p.bias;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int col = col0 + 8 * g + 4 * (lane >> 5);
+        if (p.sb_vec && col + 4 <= n_out) {
+            const f32x4 sv = p.scale_per_col ? kern::gld<f32x4>(S, (uint32_t)(col + off) * 4) : f32x4{0, 0, 0, 0};
+            const f32x4 bv = p.bias ? kern::gld<f32x4>(B, (uint32_t)(col + off) * 4) : f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                cp.s[g][e] = p.scale_per_col ? sv[e] : p.scale[0];
+                cp.b[g][e] = bv[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int cc = min(col + e, n_out - 1) + off;
+                cp.s[g][e] = p.scale[p.scale_per_col ? cc : 0];
+                cp.b[g][e] = p.bias ? p.bias[cc] : 0.0f;
+            }
+        }
+    }
+}
+
 // Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
-// `x` (and `u`), written to the wave's LDS region as rows of 32 values, then stored as 16-byte row
-// segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
+// `x` (and `u`, with `cu`), written to the wave's LDS region as rows of 32 values, then stored as
+// 16-byte row segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
 template <int EPI, int OUT>
-__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const f32x16 &u, int col0, int m_first,
-                                            int n_out, uint8_t *region, int lane) {
+__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
+                                            const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
+                                            uint8_t *region, int lane) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
     constexpr int PITCH = 32 * ESZ + 16;  // row bytes + 16: keeps 16-byte alignment, spreads banks
@@ -119,41 +153,16 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
     static_for<0, 4>([&](auto gc) {
         constexpr int g = decltype(gc)::value;
         const int c = 8 * g + 4 * h;  // first of this lane's 4 columns in the block
-        const int col = col0 + c;
-        float s1[4], b1[4] = {0, 0, 0, 0}, s2[4], b2[4] = {0, 0, 0, 0};
-        if (col + 4 <= n_out && p.scale_per_col) {
-            const f32x4 sv = *reinterpret_cast<const f32x4 *>(p.scale + col);
-            s1[0] = sv[0]; s1[1] = sv[1]; s1[2] = sv[2]; s1[3] = sv[3];
-            if (GLU) {
-                const f32x4 sw = *reinterpret_cast<const f32x4 *>(p.scale + col + p.glu_half);
-                s2[0] = sw[0]; s2[1] = sw[1]; s2[2] = sw[2]; s2[3] = sw[3];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int cc = min(col + e, n_out - 1);
-                s1[e] = p.scale_per_col ? p.scale[cc] : p.scale[0];
-                s2[e] = p.scale_per_col ? p.scale[cc + (GLU ? p.glu_half : 0)] : p.scale[0];
-            }
-        }
-        if (p.bias) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int cc = min(col + e, n_out - 1);
-                b1[e] = p.bias[cc];
-                b2[e] = GLU ? p.bias[cc + p.glu_half] : 0.0f;
-            }
-        }
         float y[4];
         static_for<0, 4>([&](auto ec) {
             constexpr int e = decltype(ec)::value;
-            float v = __fmul_rn(x[4 * g + e], s1[e]);
-            if (p.bias) v = __fadd_rn(v, b1[e]);
+            float v = __fmul_rn(x[4 * g + e], cx.s[g][e]);
+            if (has_bias) v = __fadd_rn(v, cx.b[g][e]);
             if constexpr (EPI == EPI_GELU) {
                 v = gelu_tanh(v);
             } else if constexpr (GLU) {
-                float w = __fmul_rn(u[4 * g + e], s2[e]);
-                if (p.bias) w = __fadd_rn(w, b2[e]);
+                float w = __fmul_rn(u[4 * g + e], cu.s[g][e]);
+                if (has_bias) w = __fadd_rn(w, cu.b[g][e]);
                 v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
             }
             y[e] = v;
@@ -176,18 +185,23 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
         const int m = m_first + row;
         const int col = col0 + chunk * PER;
         if (m < p.M && col < n_out) {
-            int which;
-            const int64_t off = out_index(p, m, col, which);
             if (col + PER <= n_out && p.c_vec16) {
-                *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(p.c[which]) + off * ESZ) = v;
+                int which;
+                const int64_t off = out_index(p, m, col, which);
+                *reinterpret_cast<u32x4 *>(kern::out_base(p, which) + off * ESZ) = v;
             } else {
-                const uint8_t *bytes = reinterpret_cast<const uint8_t *>(&v);
-                for (int e = 0; e < PER && col + e < n_out; ++e) {
-                    int we;
-                    const int64_t oe = out_index(p, m, col + e, we);
-                    uint8_t *oo = reinterpret_cast<uint8_t *>(p.c[we]) + oe * ESZ;
-                    for (int q = 0; q < ESZ; ++q) oo[q] = bytes[e * ESZ + q];
-                }
+                static_for<0, PER>([&](auto ec) {
+                    constexpr int e = decltype(ec)::value;
+                    if (col + e < n_out) {
+                        int we;
+                        const int64_t oe = out_index(p, m, col + e, we);
+                        uint8_t *oo = kern::out_base(p, we) + oe * ESZ;
+                        if constexpr (ESZ == 2)
+                            *reinterpret_cast<uint16_t *>(oo) = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+                        else
+                            *reinterpret_cast<uint32_t *>(oo) = v[e];
+                    }
+                });
             }
         }
     });
@@ -361,6 +375,17 @@ gemm_wd_kernel(const GemmArgs p) {
         one_step(t + 1, I1{});
     }
     if (t < KT) one_step(t, I0{});
+    // The scales and biases of the wave's columns, loaded once for all its row blocks; their latency
+    // overlaps the wait below.
+    const bool has_bias = p.bias != nullptr;
+    ColParams cp[2];
+    {
+        const int n_out = GLU ? p.glu_half : p.N;
+        static_for<0, 2>([&](auto bc) {
+            constexpr int b = decltype(bc)::value;
+            load_col_params(p, cp[b], GLU ? slab * 32 : slab * 64 + 32 * b, GLU && b == 1 ? p.glu_half : 0, n_out, lane);
+        });
+    }
     // Every wave's last (clamped) activation load has landed before any wave writes its epilogue
     // region over the stages.
     wait_vmcnt<0>();
@@ -378,7 +403,8 @@ gemm_wd_kernel(const GemmArgs p) {
             constexpr int b = decltype(bc)::value;
             const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
             if (col0 < n_out)
-                store_block<EPI, OUT>(p, acc[b][bm], acc[GLU ? 1 : b][bm], col0, m0 + 32 * bm, n_out, region, lane);
+                store_block<EPI, OUT>(p, acc[b][bm], cp[b], acc[GLU ? 1 : b][bm], cp[GLU ? 1 : b], has_bias, col0,
+                                      m0 + 32 * bm, n_out, region, lane);
         });
     });
 }
