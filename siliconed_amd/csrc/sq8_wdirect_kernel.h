@@ -266,8 +266,7 @@ gemm_wd_kernel(const GemmArgs p) {
     };
 
     // ---- fragments -----------------------------------------------------------------------------------
-    constexpr int WF = OCC == 1 ? 2 : 1;  // fragment buffers
-    bf16x8 wf[WF][2][4];                  // [buffer][block][ks]
+    bf16x8 wf[2][2][4];  // OCC = 1: [buffer][block][ks]
     auto widen_all = [&](auto src, auto dst) {
         constexpr int S = decltype(src)::value, D = decltype(dst)::value;
         static_for<0, 2>([&](auto bc) {
@@ -343,31 +342,75 @@ gemm_wd_kernel(const GemmArgs p) {
     if constexpr (OCC == 1) widen_all(I0{}, I0{});
     step_barrier();
 
-    // One step t of parity P: stage P, W(t) in raw[P] (OCC 2 widens it here; OCC 1 widened it during
-    // step t−1 and widens W(t+1) from raw[1−P] now).
-    auto one_step = [&](int t, auto par) {
+    // OCC = 2: the codes of W(t) are widened just in time, one sub-step ahead of the MFMAs that use
+    // them, like the activation fragments: two sub-steps of fragments are live at a time (the
+    // registers a full step of widened codes would take are what lets the fragment reads be
+    // double-buffered). raw[P] is free once sub-step 3 is widened: W(t+2) is issued then.
+    auto step_jit = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
-        if constexpr (OCC == 2) {
-            // Widen first and keep it first: the scheduler would otherwise sink the widening into the
-            // MFMAs and, the raw registers being read late, push the next loads to the step's end —
-            // or hoist it above the previous barrier.
-            __builtin_amdgcn_sched_barrier(0);
-            widen_all(std::integral_constant<int, P>{}, I0{});
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        issue_a(t + 1, std::integral_constant<int, 1 - P>{});
-        issue_w(t + 2, std::integral_constant<int, P>{});
+        bf16x8 wk[2][2];  // [ks & 1][block]
+        bf16x8 xf[2][FM];
+        auto widen_ks = [&](auto kc) {
+            constexpr int ks = decltype(kc)::value;
+            static_for<0, 2>([&](auto bc) {
+                constexpr int b = decltype(bc)::value;
+                const u32x4 &r = raw[P][2 * b + (ks >> 1)];
+                wk[ks & 1][b] = widen8<WT>(r[2 * (ks & 1)], r[2 * (ks & 1) + 1]);
+            });
+        };
+        auto read_x = [&](auto kc) {
+            constexpr int ks = decltype(kc)::value;
+            static_for<0, FM>([&](auto bmc) {
+                constexpr int bm = decltype(bmc)::value;
+                xf[ks & 1][bm] = kern::lds_load_frag(lds + P * SA + 32 * 128 * bm, xo[bm & 1][ks]);
+            });
+        };
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (OCC == 1) {
-            // W(t+1) must have landed before it is widened: the loads after it are this step's.
-            wait_vmcnt<A_PER_WAVE + 4>();
-            mfmas(std::integral_constant<int, P>{}, std::integral_constant<int, P>{}, std::integral_constant<int, 1 - P>{});
-        } else {
-            mfmas(std::integral_constant<int, P>{}, I0{}, I0{});
-        }
+        read_x(I0{});
+        widen_ks(I0{});
+        issue_a(t + 1, std::integral_constant<int, 1 - P>{});
+        static_for<0, 4>([&](auto kc) {
+            constexpr int ks = decltype(kc)::value;
+            if constexpr (ks < 3) {
+                read_x(std::integral_constant<int, ks + 1>{});
+                widen_ks(std::integral_constant<int, ks + 1>{});
+            }
+            if constexpr (ks == 2) {
+                // The A loads stay ahead of these in issue order (the vmcnt counts rely on it).
+                __builtin_amdgcn_sched_barrier(0);
+                issue_w(t + 2, std::integral_constant<int, P>{});
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            static_for<0, 2>([&](auto bc) {
+                constexpr int b = decltype(bc)::value;
+                static_for<0, FM>([&](auto bmc) {
+                    constexpr int bm = decltype(bmc)::value;
+                    acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wk[ks & 1][b], xf[ks & 1][bm], acc[b][bm], 0, 0, 0);
+                });
+            });
+        });
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<4>();
         step_barrier();
+    };
+
+    // One step t of parity P: stage P, W(t) in raw[P]. OCC = 1 widened W(t) during step t−1 and
+    // widens W(t+1) from raw[1−P] now.
+    auto one_step = [&](int t, auto par) {
+        constexpr int P = decltype(par)::value;
+        if constexpr (OCC == 2) {
+            step_jit(t, par);
+        } else {
+            issue_a(t + 1, std::integral_constant<int, 1 - P>{});
+            issue_w(t + 2, std::integral_constant<int, P>{});
+            __builtin_amdgcn_sched_barrier(0);
+            // W(t+1) must have landed before it is widened: the loads after it are this step's.
+            wait_vmcnt<A_PER_WAVE + 4>();
+            mfmas(std::integral_constant<int, P>{}, std::integral_constant<int, P>{}, std::integral_constant<int, 1 - P>{});
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<4>();
+            step_barrier();
+        }
     };
     int t = 0;
     for (; t + 1 < KT; t += 2) {
