@@ -19,6 +19,15 @@ hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, 
     return wl == W_NK ? launch_wdirect_1_1(p, tile, epi, out, stream) : launch_wdirect_1_2(p, tile, epi, out, stream);
 }
 
+int choose_wd_tile(int M, int N, bool glu) {
+    // 128 × 256 tiles of 64-column slabs (GLU: 32 output columns a slab). Below 96 of them (M = 1024
+    // at N = 3072, where the two kernels tie on MI355X) the skinny kernel's 32-row tiles with K split
+    // over four waves are faster: 5× at M = 1, 1.7× at M = 512.
+    const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
+    const long tiles = (long)((M + 127) / 128) * ((slabs + 3) / 4);
+    return tiles >= 96 ? WD_128 : WD_SKINNY32;
+}
+
 int choose_tile(int M, int N_out, bool glu) {
     // Tiles of 256 × 256 while they fill the 256 CUs at least 3/4 of the way; 128 × 128 below.
     const int n_virtual = glu ? 2 * N_out : N_out;

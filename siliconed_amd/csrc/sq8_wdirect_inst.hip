@@ -1,6 +1,6 @@
 // sq8_wdirect_inst.hip — instantiates the weight-direct kernels for one weight type (SQ8_WT) and
 // layout (SQ8_WL: 1 [N, K], 2 packed), compiled once per pair so the sets build in parallel.
-#include "sq8_wdirect_kernel.h"
+#include "sq8_skinny_kernel.h"
 
 #if !defined(SQ8_WT) || !defined(SQ8_WL)
 #error "compile with -DSQ8_WT=<0 int8 | 1 fp8> -DSQ8_WL=<1 [N,K] | 2 packed>"
@@ -15,6 +15,8 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
                                                                        hipStream_t stream) {
     if (tile == WD_256) return wd::dispatch_wd<256, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile == WD_SKINNY64) return wd::dispatch_skinny<64, 4, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile == WD_SKINNY32) return wd::dispatch_skinny<32, 4, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     return hipErrorInvalidValue;
 }
 

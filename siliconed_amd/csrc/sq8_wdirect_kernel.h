@@ -388,6 +388,15 @@ gemm_wd_kernel(const GemmArgs p) {
                     acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wk[ks & 1][b], xf[ks & 1][bm], acc[b][bm], 0, 0, 0);
                 });
             });
+            if constexpr (ks < 3) {
+                static_for<0, 8>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if constexpr (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if constexpr (i < 6) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
         });
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<4>();

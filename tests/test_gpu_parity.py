@@ -338,3 +338,67 @@ def test_packed_baseline_shapes(gemm, orc, case):
     y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue=name, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+# ---- every weight-direct kernel on the same problems ----------------------------------------------
+
+TILES = {"main128": "128", "main256": "256", "skinny64": "s64", "skinny32": "s32"}
+KERNEL_SHAPES = [
+    (1, 64, 64),       # one K step: three of the skinny kernel's four waves have none
+    (33, 320, 200),    # 5 K steps (not a multiple of the 4 waves), ragged M and N
+    (64, 192, 96),     # 3 K steps
+    (130, 3072, 520),
+    (512, 3072, 3072),  # the C2 skinny shape
+]
+
+
+@pytest.fixture
+def tile_knob():
+    import os
+    old = os.environ.get("SQ8_TILE")
+    yield os.environ
+    if old is None:
+        os.environ.pop("SQ8_TILE", None)
+    else:
+        os.environ["SQ8_TILE"] = old
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
+@pytest.mark.parametrize("shape", KERNEL_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_each_kernel_on_the_same_problem(gemm, orc, tile_knob, shape, fp8):
+    m, k, n = shape
+    x, q, s, b = problem(orc, m, k, n, fp8, seed=900 + m + n)
+    pk = gemm.pack(weight_tensor(q, fp8, "kn"), layout="kn", fp8=fp8 or None)
+    results = {}
+    for name, knob in TILES.items():
+        tile_knob["SQ8_TILE"] = knob
+        for out in (torch.float32, torch.bfloat16):
+            y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=out)
+            torch.cuda.synchronize()
+            judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, "gelu", out)
+            results[(name, out)] = y
+    # Same kernel, same K order: the skinny kernel gives the same bits whatever its tile height.
+    for out in (torch.float32, torch.bfloat16):
+        assert torch.equal(results[("skinny64", out)], results[("skinny32", out)])
+
+
+@pytest.mark.parametrize("epi", ["silu", "situ"])
+def test_skinny_glu_and_qkv(gemm, orc, tile_knob, epi):
+    tile_knob["SQ8_TILE"] = "s64"
+    m, k, n = 77, 640, 264  # GLU: 132 outputs, ragged against 32-column slabs
+    x, q, s, b = problem(orc, m, k, n, False, seed=41)
+    pk = gemm.pack(weight_tensor(q, False, "kn"), layout="kn", glu=True)
+    name = {"silu": "silu_glu", "situ": "situ_glu"}[epi]
+    for out in (torch.float32, torch.bfloat16):
+        y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue=name, out_dtype=out)
+        torch.cuda.synchronize()
+        judge(orc, y.float().cpu().numpy(), x, q, False, s, b, epi, out)
+    # Fused QKV through the skinny kernel, heads outermost.
+    d, hd = 256, 64
+    x, q, s, b = problem(orc, 40, 512, 3 * d, False, seed=43)
+    qo, ko, vo = gemm.product_qkv(bf16_dev(x), weight_tensor(q, False, "nk"), dev(s), layout="nk", bias=dev(b),
+                                  head_dim=hd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    full = np.concatenate([t.permute(1, 0, 2).reshape(40, d).cpu().numpy() for t in (qo, ko, vo)], axis=1)
+    judge(orc, full, x, q, False, s, b, "none", torch.float32)
+
