@@ -1,15 +1,21 @@
-"""Benchmark of the weight-quantized linear layer on one MI355X (the BASELINE.json metric).
+"""Benchmark of the weight-quantized linear layer on one MI355X.
 
-Workload (the up-projection the metric is quoted on): X bf16
-[4096, 3072] ~ N(0,1), W int8 [K=3072, N=12288] (the reference map's [K, N] layout) with codes
-uniform in [−127, 127], per-output-channel fp32 scales U(1e−3, 2e−2), bias N(0, 0.02), fused
-GELU(tanh), bf16 output. A step is one launch of the fused product on inputs already in HBM.
-Inputs are synthetic and seeded (SplitMix64 + Box–Muller, the reference's generator,
-Sources/Verification/KernelStages.swift:553-567); the seeds are in the JSON.
+Default workload — the BASELINE.json metric, configs[1]'s up-projection: X bf16 [4096, 3072] ~ N(0,1),
+W int8 [K=3072, N=12288] (the reference map's [K, N] layout) with codes uniform in [−127, 127],
+per-output-channel fp32 scales U(1e−3, 2e−2), bias N(0, 0.02), fused GELU(tanh), bf16 output.
+`--workload` selects the other configurations of the scope table (C0, C1 down, C2 fused QKV and
+skinny, C3 fp8) with the same JSON line; the driver's line is the default one.
+
+A step is one launch of the fused product on inputs already in HBM, the weight staged once by
+sq8_pack_weight (`--layout packed`, the default) or read in place. Inputs are synthetic and seeded
+(SplitMix64 + Box–Muller, the reference's generator, Sources/Verification/KernelStages.swift:553-567);
+the seeds are in the JSON.
 
 value = 2·M·N·K / (average kernel time), the kernel timed with HIP events on the stream it is
-launched on, over the timed steps. roofline.peak is MI355X's published dense bf16 MFMA rate.
-cpu_baseline: the reference's CPU route restated (Widen.dequantize → fp32 GEMM → bias → GELU,
+launched on, over the timed steps, after enough warm-up for the clocks to settle. roofline: the
+dense bf16 MFMA peak (2.5 PFLOP/s) where the arithmetic intensity is above the HBM ridge
+(2.5e15 / 8e12 = 312.5 FLOP/B), else the HBM peak (8 TB/s) on the algorithmic bytes.
+cpu_baseline: the reference's CPU route restated (Widen.dequantize → fp32 GEMM → bias → activation,
 WeightProducts.swift:698-709, Ops.swift:386-407) on a sample of the rows, run on the host cores of
 the GPU box and scaled to the whole step.
 """
@@ -26,66 +32,110 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-M, K, N = 4096, 3072, 12288
-SEEDS = {"x": 1, "w": 2, "scale": 3, "bias": 4}
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
-# HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a 512 MiB copy),
-# measured by the rocprofv3 --pmc runs in profiles/gemm_wd_kernel_c1_up_int8_packed_gelu.md, by weight layout.
-TRAFFIC_BYTES = {"packed": 483.3e6}
+RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+# HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a
+# 512 MiB copy), by (workload, weight layout), as measured by the rocprofv3 --pmc runs recorded in
+# profiles/gemm_wd_kernel_c1_up_int8_packed_gelu.md.
+TRAFFIC_BYTES = {("c1_up", "packed"): 483.3e6}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
+# name: M, K, N, weight type, epilogue, activation distribution, description.
+WORKLOADS = {
+    "c1_up": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
+              "C1 up-projection: int8 weight [K,N] per-channel fp32 scale, bf16 X, bias + fused GELU-tanh, bf16 out"),
+    "c1_down": (4096, 12288, 3072, "int8", None, "gelu",
+                "C1 down-projection on the GELU output: int8 weight, bias, bf16 out"),
+    "c0": (1024, 3072, 3072, "int8", None, "normal",
+           "C0: int8 weight [3072, 3072] per-channel scale, bias, bf16 out"),
+    "c2_qkv": (4608, 3072, 9216, "int8", "qkv", "normal",
+               "C2 fused QKV (4096 image + 512 text tokens): int8 weight [9216, 3072], bias, Q/K/V [4608, 3072] bf16"),
+    "c2_skinny": (512, 3072, 3072, "int8", None, "normal",
+                  "C2 skinny text stream: int8 weight [3072, 3072], bias, bf16 out"),
+    "c3_gate_up": (4096, 3840, 20480, "fp8", "silu_glu", "normal",
+                   "C3 fp8-e4m3 gate+up fused (2 x 10240) with SiLU-GLU, bf16 out [4096, 10240]"),
+    "c3_down": (4096, 10240, 3840, "fp8", None, "silu",
+                "C3 fp8-e4m3 down-projection [3840, 10240], bias, bf16 out"),
+    "c3_plain": (4096, 3840, 12288, "fp8", None, "normal",
+                 "C3 plain fp8-e4m3 linear W [12288, 3840], bias, bf16 out"),
+}
+SEEDS = {"x": 1, "w": 2, "scale": 3, "bias": 4}
 
-def splitmix(seed: int, count: int) -> np.ndarray:
-    """Outputs 1..count of SplitMix64 from `seed` (state_i = seed + i·γ, then the mix)."""
+
+def splitmix(seed: int, start: int, count: int) -> np.ndarray:
+    """Outputs start+1 .. start+count of SplitMix64 from `seed` (state_i = seed + i·γ, then the mix)."""
     with np.errstate(over="ignore"):
-        z = np.uint64(seed) + GAMMA * np.arange(1, count + 1, dtype=np.uint64)
+        z = np.uint64(seed) + GAMMA * np.arange(start + 1, start + count + 1, dtype=np.uint64)
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
         z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
         return z ^ (z >> np.uint64(31))
 
 
-def uniform(seed: int, count: int) -> np.ndarray:
-    return (splitmix(seed, count) >> np.uint64(11)).astype(np.float64) / 9007199254740992.0
+def uniform(seed: int, count: int, start: int = 0) -> np.ndarray:
+    return (splitmix(seed, start, count) >> np.uint64(11)).astype(np.float64) / 9007199254740992.0
 
 
-def normal(seed: int, count: int) -> np.ndarray:
-    u = uniform(seed, 2 * count)
-    u1, u2 = u[0::2], u[1::2]
-    return np.sqrt(-2.0 * np.log(np.maximum(u1, 1e-300))) * np.cos(2.0 * np.pi * u2)
+def normal_f32(seed: int, count: int, chunk: int = 1 << 24) -> np.ndarray:
+    """Box–Muller of consecutive uniform pairs, by chunks (bounded memory)."""
+    out = np.empty(count, dtype=np.float32)
+    for i in range(0, count, chunk):
+        c = min(chunk, count - i)
+        u = uniform(seed, 2 * c, start=2 * i)
+        out[i:i + c] = np.sqrt(-2.0 * np.log(np.maximum(u[0::2], 1e-300))) * np.cos(2.0 * np.pi * u[1::2])
+    return out
 
 
-def inputs():
+def inputs(workload: str):
+    """X bf16 [M, K] (a torch tensor), codes [K, N] (numpy int8) or [N, K] (torch float8_e4m3fn),
+    scales fp32 [N], bias fp32 [N]."""
     import torch
-    x = torch.from_numpy(normal(SEEDS["x"], M * K).astype(np.float32).reshape(M, K)).to(torch.bfloat16)
-    q = (np.floor(uniform(SEEDS["w"], K * N) * 255.0) - 127.0).clip(-127, 127).astype(np.int8).reshape(K, N)
-    s = (1e-3 + (2e-2 - 1e-3) * uniform(SEEDS["scale"], N)).astype(np.float32)
-    b = (0.02 * normal(SEEDS["bias"], N)).astype(np.float32)
-    return x, q, s, b
+    M, K, N, wt, epi, xdist, _ = WORKLOADS[workload]
+    x = torch.from_numpy(normal_f32(SEEDS["x"], M * K).reshape(M, K))
+    if xdist == "gelu":  # the up-projection's output
+        x = torch.nn.functional.gelu(x, approximate="tanh")
+    elif xdist == "silu":  # a SiLU-GLU output: silu(g)·u of two N(0,1)
+        u = torch.from_numpy(normal_f32(SEEDS["x"] + 100, M * K).reshape(M, K))
+        x = torch.nn.functional.silu(x) * u
+    x = x.to(torch.bfloat16)
+    b = (0.02 * normal_f32(SEEDS["bias"], N)).astype(np.float32)
+    if wt == "int8":
+        q = (np.floor(uniform(SEEDS["w"], K * N) * 255.0) - 127.0).clip(-127, 127).astype(np.int8).reshape(K, N)
+        s = (1e-3 + (2e-2 - 1e-3) * uniform(SEEDS["scale"], N)).astype(np.float32)
+        return x, q, s, b
+    # fp8: w ~ N(0, 0.02) [N, K], s_n = amax_n / 448, q = e4m3fn(RNE(w / s)) (|w / s| ≤ 448: no saturation)
+    w = torch.from_numpy(normal_f32(SEEDS["w"], N * K).reshape(N, K)) * 0.02
+    s = (w.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
+    q = (w / s[:, None]).to(torch.float8_e4m3fn)
+    return x, q, s.numpy().astype(np.float32), b
 
 
-def cpu_baseline(x_bf16, q_kn, s, b, budget_s: float = 12.0):
+def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0):
     """The reference's CPU route on a sample of rows: the whole weight widened (oracle dequantiser,
     every core), the sample's fp32 GEMM (numpy's BLAS, the cblas_sgemm of the reference), bias +
-    GELU in fp32 (oracle). Repeated for about `budget_s`; scaled to all M rows."""
+    activation in fp32 (oracle). Repeated for about `budget_s`; scaled to all M rows."""
     from oracle import oracle
+    M, K, N, wt, epi, _, _ = WORKLOADS[workload]
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    rows = 512
-    a = x_bf16[:rows].view(np.uint16)
-    a32 = oracle.bf16_to_f32(a)
+    rows = min(512, M)
+    a32 = oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
+    if wt == "int8":
+        codes, kind = q.view(np.uint8), oracle.INT8            # [K, N], scales per column
+    else:
+        codes, kind = np.ascontiguousarray(q.view(np.uint8).T), oracle.FP8_E4M3   # [N, K] → [K, N]
+    e = {"gelu_tanh": oracle.EPI_GELU_TANH, "silu_glu": oracle.EPI_SILU_GLU}.get(epi, oracle.EPI_NONE)
     t_deq, t_gemm, reps = 0.0, 0.0, 0
     start = time.perf_counter()
     while time.perf_counter() - start < budget_s or reps < 2:
         t0 = time.perf_counter()
-        w = oracle.dequantize(q_kn.view(np.uint8), oracle.INT8, s, oracle.F32, oracle.SCALE_COLUMNS, columns=N)
+        w = oracle.dequantize(codes, kind, s, oracle.F32, oracle.SCALE_COLUMNS, columns=N)
         t1 = time.perf_counter()
-        p = a32 @ w
-        y = oracle.epilogue_f32(p, bias=b, epilogue=oracle.EPI_GELU_TANH, threads=threads)
+        y = oracle.epilogue_f32(a32 @ w.reshape(K, N), bias=b, epilogue=e, threads=threads)
         t2 = time.perf_counter()
         t_deq += t1 - t0
         t_gemm += t2 - t1
         reps += 1
-        del w, p, y
+        del w, y
     t_step = t_deq / reps + (t_gemm / reps) * (M / rows)
     return {
         "value": round(2.0 * M * N * K / t_step / 1e12, 4),
@@ -93,8 +143,8 @@ def cpu_baseline(x_bf16, q_kn, s, b, budget_s: float = 12.0):
         "cores": threads,
         "kind": "port",
         "sample": (f"{rows} of {M} rows × the whole weight, {reps} repetitions in {time.perf_counter() - start:.1f} s: "
-                   f"widen {1e3 * t_deq / reps:.1f} ms + GEMM/bias/GELU {1e3 * t_gemm / reps:.1f} ms per repetition; "
-                   f"step = widen + GEMM×{M // rows}"),
+                   f"widen {1e3 * t_deq / reps:.1f} ms + GEMM/bias/activation {1e3 * t_gemm / reps:.1f} ms per "
+                   f"repetition; step = widen + GEMM×{M / rows:g}"),
         "ms_per_step": round(1e3 * t_step, 2),
     }
 
@@ -104,10 +154,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     # The clocks reach their steady state only after ~50 ms of sustained work: 10 warm-up steps leave
-    # the first timed steps 30 % slow (0.36 ms against 0.27 ms each).
+    # the first timed steps 30 % slow (0.36 ms against 0.27 ms each on the default workload).
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1_up")
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
-                    help="weight layout the product reads; packed = staged once from [K, N] by sq8_pack_weight")
+                    help="weight layout the product reads; packed = staged once by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the product, copy MIB MiB device→device --steps times (the known-size kernel "
@@ -131,25 +182,42 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": nbytes, "launches": args.steps}), flush=True)
         return 0
-    x, q_kn, s, b = inputs()
-    q = np.ascontiguousarray(q_kn.T) if args.layout == "nk" else q_kn
+
+    M, K, N, wt, epi, _, desc = WORKLOADS[args.workload]
+    fp8 = wt == "fp8"
+    glu = epi == "silu_glu"
+    qkv = epi == "qkv"
+    x, q, s, b = inputs(args.workload)
     xd = x.to(dev)
-    wd = torch.from_numpy(q).to(dev)
     sd = torch.from_numpy(s).to(dev)
     bd = torch.from_numpy(b).to(dev)
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ctx = sq.context(0)
+    if fp8:
+        wd, lay = q.to(dev), "nk"                           # [N, K] e4m3fn codes (packed from [N, K])
+        if args.layout == "kn":
+            wd, lay = wd.t().contiguous(), "kn"
+    else:
+        wd, lay = torch.from_numpy(q).to(dev), "kn"         # [K, N] int8 codes (packed from [K, N])
+        if args.layout == "nk":
+            wd, lay = wd.t().contiguous(), "nk"
     stage_ms = None
     if args.layout == "packed":
         torch.cuda.synchronize()
         t_stage = time.perf_counter()
-        wd = ctx.pack(wd, layout="kn")
+        wd = ctx.pack(wd, layout=lay, glu=glu)
         torch.cuda.synchronize()
         stage_ms = 1e3 * (time.perf_counter() - t_stage)
-    layout = "nk" if args.layout == "nk" else "kn"
+    n_out = N // 2 if glu else N
+    if qkv:
+        outs = tuple(torch.empty((M, N // 3), dtype=torch.bfloat16, device=dev) for _ in range(3))
 
-    def step():
-        ctx.product(xd, wd, sd, layout=layout, bias=bd, epilogue="gelu_tanh", out=out)
+        def step():
+            ctx.product_qkv(xd, wd, sd, layout=lay, bias=bd, out=outs)
+    else:
+        out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
 
     for _ in range(args.warmup):
         step()
@@ -166,11 +234,25 @@ def main() -> int:
     kernel_ms = ev0.elapsed_time(ev1) / args.steps
     flops = 2.0 * M * N * K
     tflops = flops / (kernel_ms * 1e-3) / 1e12
-    algo_bytes = 2 * M * K + N * K + 4 * N + 4 * N + 2 * M * N
+    algo_bytes = 2 * M * K + N * K + 4 * N + 4 * N + 2 * M * n_out
+    intensity = flops / algo_bytes
+    gbs = algo_bytes / (kernel_ms * 1e-3) / 1e9
+    if intensity >= RIDGE:
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    roofline.update({"traffic": TRAFFIC_BYTES.get((args.workload, args.layout)), "algorithmic_bytes": algo_bytes,
+                     "flops": flops, "intensity_flop_per_byte": round(intensity, 1),
+                     "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5),
+                     "mfma_bound_ms": round(flops / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 5)})
 
     props = torch.cuda.get_device_properties(0)
+    metric = ("TFLOP/s and % bf16 MFMA peak, int8-weight GEMM 4096x3072x12288 on 1 MI355X" if args.workload == "c1_up"
+              else f"TFLOP/s and % bf16 MFMA peak, {wt}-weight GEMM {M}x{K}x{N} on 1 MI355X")
     result = {
-        "metric": "TFLOP/s and % bf16 MFMA peak, int8-weight GEMM 4096x3072x12288 on 1 MI355X",
+        "metric": metric,
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -182,22 +264,18 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}",
-        "config": {"workload": "C1 up-projection: int8 weight [K,N] per-channel fp32 scale, bf16 X, bias + fused "
-                               "GELU-tanh, bf16 out",
-                   "M": M, "K": K, "N": N, "weight_layout": args.layout.upper(),
+        "config": {"workload": f"{args.workload}: {desc}", "M": M, "K": K, "N": N, "weight_type": wt,
+                   "weight_layout": args.layout.upper(),
                    "staging_ms": None if stage_ms is None else round(stage_ms, 3), "global_batch": M,
                    "parallelism": "none (one GPU)"},
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kernel_ms, 5),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC_BYTES.get(args.layout),
-                     "algorithmic_bytes": algo_bytes,
-                     "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5)},
+        "roofline": roofline,
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(x.view(torch.int16).numpy(), q_kn, s, b)
+        xb = x.view(torch.int16).numpy()
+        result["cpu_baseline"] = cpu_baseline(args.workload, xb, q.view(torch.uint8).numpy() if fp8 else q, s, b)
     print(json.dumps(result), flush=True)
     return 0
 

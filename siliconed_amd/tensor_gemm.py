@@ -248,9 +248,9 @@ class TensorGEMM:
 
     def product_qkv(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
                     bias: Optional[torch.Tensor] = None, head_dim: int = 0,
-                    out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None):
+                    out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None, out=None):
         """Fused QKV: W of 3·d output channels; returns (q, k, v), each [m, d] (head_dim 0) or
-        [d/head_dim, m, head_dim]."""
+        [d/head_dim, m, head_dim]. `out`: three preallocated tensors of that shape (contiguous)."""
         m, k = x.shape
         if isinstance(w, PackedWeight):
             lay, wd, n, ldw, wptr = w.layout, w.w_dtype, w.n, w.k, _dev(w.data, "w")
@@ -263,7 +263,14 @@ class TensorGEMM:
             raise ValueError("a fused QKV weight has 3·d output channels")
         d = n // 3
         shape = (m, d) if head_dim == 0 else (d // head_dim, m, head_dim)
-        q, kk, v = (torch.empty(shape, dtype=out_dtype, device=x.device) for _ in range(3))
+        if out is None:
+            q, kk, v = (torch.empty(shape, dtype=out_dtype, device=x.device) for _ in range(3))
+        else:
+            q, kk, v = out
+            for t in out:
+                if tuple(t.shape) != shape or not t.is_contiguous() or t.dtype not in (torch.bfloat16, torch.float32):
+                    raise ValueError(f"QKV outputs must be contiguous {shape} bf16/fp32 tensors")
+            out_dtype = q.dtype
         per_col = scale.numel() != 1
         st = abi.load().sq8_linear_qkv(
             self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
