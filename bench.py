@@ -149,6 +149,46 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0):
     }
 
 
+def dit_block(args) -> int:
+    """C4: one synthetic single-stream DiT block forward (siliconed_amd.dit_block): hidden 3072, 24
+    heads of 128, 4096 image + 512 text tokens, int8 per-channel modulation / QKV / out / MLP-4×
+    weights, bf16 attention, fp32 residual. value: the block's TFLOP/s (linear + attention FLOPs)."""
+    import torch
+    from siliconed_amd.dit_block import DiTBlock
+    S, d, heads = 4096 + 512, 3072, 24
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=SEEDS["w"])
+    x = torch.from_numpy(normal_f32(SEEDS["x"], S * d).reshape(S, d)).cuda()
+    temb = torch.from_numpy(normal_f32(SEEDS["bias"], d)).cuda()
+    for _ in range(max(args.warmup // 20, 5)):
+        blk.forward(x, temb)
+    torch.cuda.synchronize()
+    steps = max(args.steps // 5, 5)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        blk.forward(x, temb)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1) / steps
+    flops = blk.flops(S)
+    tflops = flops / (ms * 1e-3) / 1e12
+    result = {
+        "metric": "DiT block forward ms (hidden 3072, 24x128 heads, 4608 tokens, int8 weights) on 1 MI355X",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "block_ms": round(ms, 4), "n_gpus": 1, "steps": steps,
+        "warmup": max(args.warmup // 20, 5), "ms_per_step": round(1e3 * wall / steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": f"synthetic, seeded: x, temb SplitMix64 + Box-Muller; weights torch generator seed {SEEDS['w']}",
+        "config": {"workload": "c4_block: one single-stream DiT block (modulation, RMSNorm, fused QKV, qk-RMSNorm, "
+                               "SDPA, Wo, GELU MLP 4x, gated residuals)", "tokens": S, "hidden": d, "heads": heads,
+                   "flops": flops, "global_batch": S, "parallelism": "none (one GPU)"},
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,7 +196,7 @@ def main() -> int:
     # The clocks reach their steady state only after ~50 ms of sustained work: 10 warm-up steps leave
     # the first timed steps 30 % slow (0.36 ms against 0.27 ms each on the default workload).
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c1_up")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4_block"], default="c1_up")
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -183,6 +223,8 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": nbytes, "launches": args.steps}), flush=True)
         return 0
 
+    if args.workload == "c4_block":
+        return dit_block(args)
     M, K, N, wt, epi, _, desc = WORKLOADS[args.workload]
     fp8 = wt == "fp8"
     glu = epi == "silu_glu"

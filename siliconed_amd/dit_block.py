@@ -1,0 +1,123 @@
+"""A synthetic single-stream DiT block on the weight-quantized linear layer: the C4 workload.
+
+One block of MossImage.swift:15-19 with the 4× GELU-tanh MLP of the other DiT targets:
+
+    n = RMS(x)·w_a·(1 + scale_a) + shift_a
+    x += gate_a · Wo( SDPA(RMS_h(Wq n), RMS_h(Wk n), Wv n) )        (heads of 128, no mask)
+    m = RMS(x)·w_f·(1 + scale_f) + shift_f
+    x += gate_f · W_down( GELU_tanh(W_up m) )
+
+with the six modulation vectors [shift_a, scale_a, gate_a, shift_f, scale_f, gate_f] from one Linear
+of the timestep embedding (MossImage.swift:23-27: no SiLU before it, the shift first, plain gates).
+Every Linear — the modulation, the fused QKV, Wo, W_up (GELU fused) and W_down — is an int8
+per-output-channel product of this library (weights w ~ N(0, 0.02), s = amax/127,
+q = clamp(rint(w/s), −127, 127), staged once in the packed layout). The residual stream is fp32 as
+in the reference; the products' operands are bf16. The norms (eps 1e-6, MossImage.swift:49), the
+residual updates and the attention (torch's fused flash / memory-efficient SDPA in bf16) are torch.
+RoPE is left out: an elementwise rotation of q and k, small next to the products.
+"""
+from __future__ import annotations
+
+import torch
+
+from .tensor_gemm import TensorGEMM, context
+
+EPS = 1e-6
+
+
+def quantize_int8(w: torch.Tensor):
+    """Per-output-channel int8 of an [N, K] weight: s = amax/127, q = clamp(rint(w/s), −127, 127)."""
+    s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-30)
+    q = torch.round(w / s[:, None]).clamp(-127, 127).to(torch.int8)
+    return q, s.float()
+
+
+def rms_modulate(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
+    """RMS(x)·w·(1 + scale) + shift, fp32 arithmetic, bf16 result (the next product's operand)."""
+    r = torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + EPS)
+    return ((x * r) * w * (1.0 + scale) + shift).to(torch.bfloat16)
+
+
+def rms_heads(t: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Per-head RMSNorm of q or k, [heads, S, head_dim] bf16, fp32 arithmetic."""
+    t32 = t.float()
+    return (t32 * torch.rsqrt(t32.pow(2).mean(dim=-1, keepdim=True) + EPS) * w).to(torch.bfloat16)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Softmax attention of [heads, S, head_dim] bf16, no mask, on torch's fused kernels only."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        return torch.nn.functional.scaled_dot_product_attention(q[None], k[None], v[None])[0]
+
+
+class DiTBlock:
+    """The block's weights (int8 packed, fp32 scales, fp32 norm weights) on one device."""
+
+    def __init__(self, d: int = 3072, heads: int = 24, mlp: int = 4, seed: int = 0, device: int = 0,
+                 ctx: TensorGEMM | None = None):
+        if d % heads or (d // heads) % 8:
+            raise ValueError("d must split into heads of a multiple of 8")
+        self.d, self.heads, self.hd = d, heads, d // heads
+        self.ctx = ctx or context(device)
+        dev = torch.device("cuda", device)
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def linear(n_out: int, k: int):
+            w = torch.randn((n_out, k), device=dev, generator=g) * 0.02
+            q, s = quantize_int8(w)
+            b = torch.randn(n_out, device=dev, generator=g) * 0.02
+            return {"w": w, "q": q, "s": s, "b": b, "packed": self.ctx.pack(q, layout="nk")}
+
+        self.mod = linear(6 * d, d)
+        self.qkv = linear(3 * d, d)
+        self.out = linear(d, d)
+        self.up = linear(mlp * d, d)
+        self.down = linear(d, mlp * d)
+        self.norm_a = 1.0 + 0.02 * torch.randn(d, device=dev, generator=g)
+        self.norm_f = 1.0 + 0.02 * torch.randn(d, device=dev, generator=g)
+        self.norm_q = 1.0 + 0.02 * torch.randn(self.hd, device=dev, generator=g)
+        self.norm_k = 1.0 + 0.02 * torch.randn(self.hd, device=dev, generator=g)
+
+    def _product(self, x: torch.Tensor, lin: dict, epilogue=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+        return self.ctx.product(x, lin["packed"], lin["s"], bias=lin["b"], epilogue=epilogue, out_dtype=out_dtype)
+
+    def forward(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+        """x fp32 [S, d] (the residual stream), temb [d]: the block's output, fp32 [S, d]."""
+        S, d = x.shape
+        mod = self._product(temb.to(torch.bfloat16)[None], self.mod, out_dtype=torch.float32)[0]
+        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
+        n = rms_modulate(x, self.norm_a, scale_a, shift_a)
+        q, k, v = self.ctx.product_qkv(n, self.qkv["packed"], self.qkv["s"], bias=self.qkv["b"], head_dim=self.hd)
+        o = attention(rms_heads(q, self.norm_q), rms_heads(k, self.norm_k), v)   # [heads, S, hd]
+        o = o.transpose(0, 1).reshape(S, d)
+        x = x + gate_a * self._product(o, self.out, out_dtype=torch.float32)
+        m = rms_modulate(x, self.norm_f, scale_f, shift_f)
+        h = self._product(m, self.up, epilogue="gelu_tanh")
+        return x + gate_f * self._product(h, self.down, out_dtype=torch.float32)
+
+    def reference(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+        """The same block in fp32 with the dequantised weights (Float(q)·s) and fp32 math attention:
+        the check of `forward` (operands rounded to bf16 where `forward` rounds them)."""
+        def lin(a, L, act=None):
+            y = a.float() @ (L["q"].float() * L["s"][:, None]).t() + L["b"]
+            return torch.nn.functional.gelu(y, approximate="tanh") if act else y
+        S, d = x.shape
+        mod = lin(temb.to(torch.bfloat16)[None], self.mod)[0]
+        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
+        n = rms_modulate(x, self.norm_a, scale_a, shift_a)
+        qkv = lin(n, self.qkv).to(torch.bfloat16).view(S, 3, self.heads, self.hd).permute(1, 2, 0, 3)
+        q, k, v = (rms_heads(t.contiguous(), w).float() if w is not None else t.float()
+                   for t, w in zip(qkv, (self.norm_q, self.norm_k, None)))
+        att = torch.softmax((q @ k.transpose(1, 2).contiguous()) / self.hd ** 0.5, dim=-1) @ v
+        o = att.to(torch.bfloat16).transpose(0, 1).reshape(S, d)
+        x = x + gate_a * lin(o, self.out)
+        m = rms_modulate(x, self.norm_f, scale_f, shift_f)
+        h = lin(m, self.up, act=True).to(torch.bfloat16)
+        return x + gate_f * lin(h, self.down)
+
+    def flops(self, S: int) -> float:
+        """Linear FLOPs (modulation included) + attention's two products."""
+        d = self.d
+        lin = 2.0 * (6 * d * d + S * (3 * d * d + d * d + 2 * self.up["q"].shape[0] * d))
+        return lin + 4.0 * S * S * d
