@@ -18,6 +18,8 @@ struct sq8_ctx {
     hipEvent_t begin, end;
     void *scratch;          // bf16 copy of an fp32 activation (the reference's rounding scratch)
     size_t scratch_bytes;
+    void *wpack;            // [K, N] codes repacked for the weight-direct kernels, per product
+    size_t wpack_bytes;
 };
 
 namespace {
@@ -56,6 +58,20 @@ int check_config(int a_dtype, int w_dtype, int w_layout, int scale_layout, int c
 }
 
 // Grows the rounding scratch to `bytes` (never shrinks; freed with the context).
+// Grows a context buffer (after the stream has finished with the old one).
+int reserve_buffer(sq8_ctx *ctx, void **buf, size_t *have, size_t bytes) {
+    if (*have >= bytes) return SQ8_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+    if (*buf) (void)hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+    e = hipMalloc(buf, bytes);
+    if (e != hipSuccess) { *buf = nullptr; return hip_status(e); }
+    *have = bytes;
+    return SQ8_OK;
+}
+
 int reserve_scratch(sq8_ctx *ctx, size_t bytes) {
     if (ctx->scratch_bytes >= bytes) return SQ8_OK;
     if (ctx->scratch) {
@@ -173,10 +189,25 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     const bool k_steps = q.k > 0 && (q.k % 64) == 0;
     p.kt = (q.k + 63) / 64;
     hipError_t e;
-    if (is_packed(q.w_layout) || (q.w_layout == SQ8_NK && p.a_vec && p.w_vec && k_steps && cols_per_half >= 1)) {
+    // [K, N] codes in place: repacked per product into the context's buffer when the repack runs near
+    // the memory bandwidth (the reference's in-place route, Artifact.swift:443-459, at the speed of
+    // the staged one: 37.7 MB of C1 codes cost ~12 µs against ~230 µs saved).
+    int wl_run = q.w_layout;
+    if (q.w_layout == SQ8_KN && p.a_vec && k_steps &&
+        sq8::pack_is_fast(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue))) {
+        const int64_t bytes = sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue));
+        st = reserve_buffer(ctx, &ctx->wpack, &ctx->wpack_bytes, (size_t)bytes);
+        if (st != SQ8_OK) return st;
+        e = sq8::launch_pack(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue), static_cast<uint8_t *>(ctx->wpack),
+                             ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        p.w = static_cast<const uint8_t *>(ctx->wpack);
+        wl_run = is_glu(q.epilogue) ? SQ8_PACKED_GLU : SQ8_PACKED;
+    }
+    if (is_packed(wl_run) || (q.w_layout == SQ8_NK && p.a_vec && p.w_vec && k_steps && cols_per_half >= 1)) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
-        const int wl = is_packed(q.w_layout) ? sq8::W_PACKED : sq8::W_NK;
+        const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
         int tile = sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
         const char *force = getenv("SQ8_TILE");  // measurement knob: "256", "128", "s64", "s32"
         if (force && strcmp(force, "256") == 0) tile = sq8::WD_256;
@@ -254,6 +285,7 @@ int sq8_destroy(sq8_ctx *ctx) {
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) st = hip_status(e);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->wpack) (void)hipFree(ctx->wpack);
     (void)hipEventDestroy(ctx->begin);
     (void)hipEventDestroy(ctx->end);
     delete ctx;

@@ -79,14 +79,64 @@ __global__ void __launch_bounds__(256) pack_kernel(const uint8_t *__restrict__ w
             valid = col < n;
         }
         const int k0 = 64 * t + 32 * h + 16 * (j & 1);
-        uint32_t d[4] = {0, 0, 0, 0};
-        for (int e = 0; e < 16; ++e) {
-            const int kk = k0 + e;
-            uint32_t v = 0;
-            if (valid && kk < k) v = wl == W_KN ? w[(int64_t)kk * ldw + col] : w[(int64_t)col * ldw + kk];
-            d[e >> 2] |= v << (8 * (e & 3));
+        u32x4 v = {0, 0, 0, 0};
+        if (valid && wl == W_NK && k0 + 16 <= k && (ldw & 15) == 0 && ((uintptr_t)w & 15) == 0) {
+            // [N, K]: the chunk is 16 contiguous codes of row `col`.
+            v = *reinterpret_cast<const u32x4 *>(w + (int64_t)col * ldw + k0);
+        } else {
+            uint32_t d[4] = {0, 0, 0, 0};
+            for (int e = 0; e < 16; ++e) {
+                const int kk = k0 + e;
+                uint32_t x = 0;
+                if (valid && kk < k) x = wl == W_KN ? w[(int64_t)kk * ldw + col] : w[(int64_t)col * ldw + kk];
+                d[e >> 2] |= x << (8 * (e & 3));
+            }
+            v = u32x4{d[0], d[1], d[2], d[3]};
         }
-        *reinterpret_cast<u32x4 *>(out + c * 16) = u32x4{d[0], d[1], d[2], d[3]};
+        *reinterpret_cast<u32x4 *>(out + c * 16) = v;
+    }
+}
+
+// [K, N] codes, full tiles: one workgroup per (slab, 4 K steps) — 256 rows of K × the slab's 64
+// (virtual) columns. Each thread loads 4 consecutive rows × 16 columns (four 16-byte loads),
+// transposes the 4 × 16 bytes in registers into 16 words of 4 consecutive K of one column, and
+// writes them to an LDS tile [column][K]; the packed chunks (16 consecutive K of one column) are then
+// 16-byte LDS reads. Requires k % 256 == 0, whole slabs (n % 64 == 0, GLU: half % 32 == 0), ldw %
+// 16 == 0 and a 16-byte aligned base.
+constexpr int PK_KSTEPS = 4;
+constexpr int PK_PITCH = 64 * PK_KSTEPS + 16;  // bytes per LDS column row (16-byte aligned, bank spread)
+
+__device__ __forceinline__ uint32_t byte_of(const u32x4 &v, int e) { return (v[e >> 2] >> (8 * (e & 3))) & 0xFF; }
+
+__global__ void __launch_bounds__(256) pack_kn_kernel(const uint8_t *__restrict__ w, int64_t ldw, int n, int glu, int kt,
+                                                      uint8_t *__restrict__ out) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[64 * PK_PITCH];
+    const int groups = kt / PK_KSTEPS;
+    const int slab = blockIdx.x / groups, tq = blockIdx.x - slab * groups;
+    const int tid = threadIdx.x;
+    const int seg = tid & 3, kq = tid >> 2;  // columns [16·seg, +16) of the slab, rows 4·kq .. 4·kq + 3
+    const int vc0 = 16 * seg, b = vc0 >> 5;
+    const int col0 = glu ? slab * 32 + (vc0 & 31) + b * (n / 2) : slab * 64 + vc0;
+    const uint8_t *src = w + (int64_t)(tq * 64 * PK_KSTEPS + 4 * kq) * ldw + col0;
+    u32x4 r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const u32x4 *>(src + i * ldw);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t word = byte_of(r[0], e) | byte_of(r[1], e) << 8 | byte_of(r[2], e) << 16 | byte_of(r[3], e) << 24;
+        *reinterpret_cast<uint32_t *>(tile + (vc0 + e) * PK_PITCH + 4 * kq) = word;
+    }
+    __syncthreads();
+    // 4 K steps × 4 loads × 64 lanes = 1024 chunks, 4 per thread.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;
+        const int lane = c & 63, j = (c >> 6) & 3, ts = c >> 8;
+        const int vc = 32 * (j >> 1) + (lane & 31);
+        const int kr = 64 * ts + 32 * (lane >> 5) + 16 * (j & 1);
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + vc * PK_PITCH + kr);
+        const int t = tq * PK_KSTEPS + ts;
+        *reinterpret_cast<u32x4 *>(out + (((int64_t)slab * kt + t) * 4 + j) * 1024 + lane * 16) = v;
     }
 }
 
@@ -98,10 +148,22 @@ int64_t packed_bytes(int k, int n, bool glu) {
     return slabs * kt * 4096;
 }
 
+bool pack_is_fast(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu) {
+    const bool whole_slabs = glu ? (n % 2 == 0 && (n / 2) % 32 == 0) : n % 64 == 0;
+    return wl == W_KN && k > 0 && k % (64 * PK_KSTEPS) == 0 && n > 0 && whole_slabs && ldw % 16 == 0 &&
+           ((uintptr_t)w & 15) == 0;
+}
+
 hipError_t launch_pack(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu, uint8_t *out, hipStream_t stream) {
     const int kt = (k + 63) / 64;
     const int64_t chunks = packed_bytes(k, n, glu) / 16;
     if (chunks == 0) return hipSuccess;
+    if (pack_is_fast(w, wl, ldw, k, n, glu)) {
+        const int64_t slabs = glu ? (n / 2) / 32 : n / 64;
+        hipLaunchKernelGGL(pack_kn_kernel, dim3((unsigned)(slabs * (kt / PK_KSTEPS))), dim3(256), 0, stream, w, ldw, n,
+                           glu ? 1 : 0, kt, out);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(pack_kernel, dim3(grid_for(chunks)), dim3(256), 0, stream, w, wl, ldw, k, n, glu ? 1 : 0, kt,
                        chunks, out);
     return hipGetLastError();

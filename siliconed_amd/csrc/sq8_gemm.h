@@ -52,6 +52,9 @@ hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, 
 // Bytes of the packed layout of a weight with k rows of K and n columns (GLU: n = 2h, packed in
 // pairs of 32-column blocks of the two halves).
 int64_t packed_bytes(int k, int n, bool glu);
+// True when launch_pack has its LDS-transposing path for these [K, N] codes (k % 256 == 0, whole
+// 64-column slabs, 16-byte aligned rows): a repack runs near the memory bandwidth.
+bool pack_is_fast(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu);
 // Writes the packed layout of codes `w` (layout W_KN or W_NK, leading dimension ldw) into `out`.
 hipError_t launch_pack(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu, uint8_t *out,
                        hipStream_t stream);
