@@ -163,6 +163,28 @@ int sq8_dequantize(sq8_ctx *ctx, const void *codes, int w_dtype, int64_t rows, i
  * Replaces: the `round_bf16` pass (TensorGEMMBF16.swift:41-48, 67-73). */
 int sq8_round_bf16(sq8_ctx *ctx, const float *x, uint16_t *y, int64_t count);
 
+/* ---- the elementwise passes of a DiT block around the products (all device pointers, queued) ---- */
+
+/* **Modulated RMSNorm to the next product's operand**: for each of `rows` rows of fp32 x (leading
+ * dimension `ldx`), out = bf16(((x·r)·w)·(1 + scale) + shift) with r = 1/sqrt(mean(x²) + eps), every
+ * product and sum rounded on its own; w, scale, shift fp32 [cols]; out bf16, leading dimension `ldo`.
+ * Replaces: `norm_modulate_rounded` (Sources/Siliconed/ElementwiseGPUMoss.swift:45-91), the
+ * `modulatedNorm` of a MOSS block (MossImage.swift:399, :418). */
+int sq8_norm_modulate(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                      const float *shift, float eps, uint16_t *out, int64_t ldo, int rows, int cols);
+
+/* **Per-row RMSNorm in place** of bf16 rows of `cols` ≤ 256 values (the heads of q or k):
+ * t = bf16((t·r)·w), r = 1/sqrt(mean(t²) + eps), w fp32 [cols]. Replaces: the per-head RMSNorm of
+ * q and k (`RMS_h`, MossImage.swift:15-19). */
+int sq8_rms_rows(sq8_ctx *ctx, uint16_t *t, int64_t ld, int64_t rows, int cols, const float *w, float eps);
+
+/* **Gated residual update**: x[r, c] += gate[c] · y[r, c] (the product rounded, then the sum) over
+ * `rows` × `cols`; x fp32 (leading dimension `ldx`), y `y_dtype` SQ8_BF16 or SQ8_F32 (`ldy`), gate
+ * fp32 [cols] or NULL (1). Replaces: `x += gate · …` of a DiT block (MossImage.swift:15-19), the
+ * residual loop of `residual_modulate` (ElementwiseGPUAnima.swift:47-62). */
+int sq8_gated_residual(sq8_ctx *ctx, float *x, int64_t ldx, const void *y, int y_dtype, int64_t ldy,
+                       const float *gate, int64_t rows, int cols);
+
 /* Waits for everything queued on the context's stream. Replaces: waitUntilCompleted /
  * GPUStream.drain (GPUStream.swift). */
 int sq8_synchronize(sq8_ctx *ctx);

@@ -33,6 +33,9 @@ SIGNATURES = {
     "sq8_pack_weight": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P]),
     "sq8_dequantize": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _I, _I64, _I64, _P]),
     "sq8_round_bf16": (_I, [_P, _P, _P, _I64]),
+    "sq8_norm_modulate": (_I, [_P, _P, _I64, _P, _P, _P, ctypes.c_float, _P, _I64, _I, _I]),
+    "sq8_rms_rows": (_I, [_P, _P, _I64, _I64, _I, _P, ctypes.c_float]),
+    "sq8_gated_residual": (_I, [_P, _P, _I64, _P, _I, _I64, _P, _I64, _I]),
     "sq8_synchronize": (_I, [_P]),
     "sq8_status_string": (ctypes.c_char_p, [_I]),
     "sq8_abi_version": (_I, []),

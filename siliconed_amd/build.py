@@ -31,6 +31,7 @@ SOURCES = [
     ("sq8_wdirect_inst.hip", "sq8_wdirect_f8_nk", ["-DSQ8_WT=1", "-DSQ8_WL=1"]),
     ("sq8_wdirect_inst.hip", "sq8_wdirect_f8_packed", ["-DSQ8_WT=1", "-DSQ8_WL=2"]),
     ("sq8_aux.hip", "sq8_aux", []),
+    ("sq8_block.hip", "sq8_block", []),
     ("sq8_api.hip", "sq8_api", []),
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -44,6 +45,10 @@ FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Every product and sum rounded on its own, as the reference's kernels (`fp contract(off)`): HIP
+    # contracts a·b + c into one FMA by default, and its __fmul_rn / __fadd_rn are plain operators.
+    # Where a fused multiply-add is meant, the code says __builtin_fmaf.
+    "-ffp-contract=off",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]

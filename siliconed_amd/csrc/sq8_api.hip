@@ -381,6 +381,37 @@ int sq8_round_bf16(sq8_ctx *ctx, const float *x, uint16_t *y, int64_t count) {
     return hip_status(sq8::launch_round_bf16(x, y, count, ctx->stream));
 }
 
+int sq8_norm_modulate(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                      const float *shift, float eps, uint16_t *out, int64_t ldo, int rows, int cols) {
+    if (!ctx || rows < 0 || cols < 0) return SQ8_EINVAL;
+    if (rows == 0 || cols == 0) return SQ8_OK;
+    if (!x || !w || !scale || !shift || !out || ldx < cols || ldo < cols || !(eps >= 0.0f)) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_norm_modulate(x, ldx, w, scale, shift, eps, out, ldo, rows, cols, ctx->stream));
+}
+
+int sq8_rms_rows(sq8_ctx *ctx, uint16_t *t, int64_t ld, int64_t rows, int cols, const float *w, float eps) {
+    if (!ctx || rows < 0 || cols < 0) return SQ8_EINVAL;
+    if (rows == 0 || cols == 0) return SQ8_OK;
+    if (!t || !w || ld < cols || !(eps >= 0.0f)) return SQ8_EINVAL;
+    if (cols > 256) return SQ8_EUNSUPPORTED;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_rms_rows(t, ld, rows, cols, w, eps, ctx->stream));
+}
+
+int sq8_gated_residual(sq8_ctx *ctx, float *x, int64_t ldx, const void *y, int y_dtype, int64_t ldy,
+                       const float *gate, int64_t rows, int cols) {
+    if (!ctx || rows < 0 || cols < 0) return SQ8_EINVAL;
+    if (rows == 0 || cols == 0) return SQ8_OK;
+    if (!x || !y || ldx < cols || ldy < cols) return SQ8_EINVAL;
+    if (y_dtype != SQ8_BF16 && y_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_gated_residual(x, ldx, y, y_dtype == SQ8_BF16, ldy, gate, rows, cols, ctx->stream));
+}
+
 int sq8_synchronize(sq8_ctx *ctx) {
     if (!ctx) return SQ8_EINVAL;
     DeviceScope scope(ctx->device);

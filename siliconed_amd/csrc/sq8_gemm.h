@@ -65,4 +65,11 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
                              hipStream_t stream);
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
 
+// The DiT block's elementwise passes (sq8_block.hip).
+hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,
+                                float eps, uint16_t *out, int64_t ldo, int rows, int cols, hipStream_t stream);
+hipError_t launch_rms_rows(uint16_t *t, int64_t ld, int64_t rows, int cols, const float *w, float eps, hipStream_t stream);
+hipError_t launch_gated_residual(float *x, int64_t ldx, const void *y, bool y_bf16, int64_t ldy, const float *gate,
+                                 int64_t rows, int cols, hipStream_t stream);
+
 }  // namespace sq8

@@ -12,9 +12,10 @@ of the timestep embedding (MossImage.swift:23-27: no SiLU before it, the shift f
 Every Linear — the modulation, the fused QKV, Wo, W_up (GELU fused) and W_down — is an int8
 per-output-channel product of this library (weights w ~ N(0, 0.02), s = amax/127,
 q = clamp(rint(w/s), −127, 127), staged once in the packed layout). The residual stream is fp32 as
-in the reference; the products' operands are bf16. The norms (eps 1e-6, MossImage.swift:49), the
-residual updates and the attention (torch's fused flash / memory-efficient SDPA in bf16) are torch.
-RoPE is left out: an elementwise rotation of q and k, small next to the products.
+in the reference; the products' operands are bf16. The modulated norms (eps 1e-6, MossImage.swift:49),
+the per-head norms and the gated residual updates are this library's elementwise passes; the
+attention is torch's fused flash / memory-efficient SDPA in bf16. RoPE is left out: an elementwise
+rotation of q and k, small next to the products.
 """
 from __future__ import annotations
 
@@ -82,19 +83,31 @@ class DiTBlock:
     def _product(self, x: torch.Tensor, lin: dict, epilogue=None, out_dtype=torch.bfloat16) -> torch.Tensor:
         return self.ctx.product(x, lin["packed"], lin["s"], bias=lin["b"], epilogue=epilogue, out_dtype=out_dtype)
 
-    def forward(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
-        """x fp32 [S, d] (the residual stream), temb [d]: the block's output, fp32 [S, d]."""
+    def forward_(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+        """The block on the residual stream x (fp32 [S, d], contiguous), updated in place as the
+        reference's stream buffer is; temb [d]. Every pass but the attention is this library's: the
+        modulation, the fused QKV (rows [S, heads·hd]: q, k, v are [heads, S, hd] views), Wo, W_up with
+        GELU fused and W_down products; the modulated norms, the per-head norms of q and k and the
+        gated residual updates."""
         S, d = x.shape
+        ctx = self.ctx
         mod = self._product(temb.to(torch.bfloat16)[None], self.mod, out_dtype=torch.float32)[0]
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
-        n = rms_modulate(x, self.norm_a, scale_a, shift_a)
-        q, k, v = self.ctx.product_qkv(n, self.qkv["packed"], self.qkv["s"], bias=self.qkv["b"], head_dim=self.hd)
-        o = attention(rms_heads(q, self.norm_q), rms_heads(k, self.norm_k), v)   # [heads, S, hd]
-        o = o.transpose(0, 1).reshape(S, d)
-        x = x + gate_a * self._product(o, self.out, out_dtype=torch.float32)
-        m = rms_modulate(x, self.norm_f, scale_f, shift_f)
+        n = ctx.norm_modulate(x, self.norm_a, scale_a, shift_a, EPS)
+        q, k, v = ctx.product_qkv(n, self.qkv["packed"], self.qkv["s"], bias=self.qkv["b"])   # [S, d] each
+        ctx.rms_rows(q.view(S * self.heads, self.hd), self.norm_q, EPS)
+        ctx.rms_rows(k.view(S * self.heads, self.hd), self.norm_k, EPS)
+        heads = lambda t: t.view(S, self.heads, self.hd).transpose(0, 1)                        # [heads, S, hd]
+        o = attention(heads(q), heads(k), heads(v)).transpose(0, 1).reshape(S, d)
+        ctx.gated_residual(x, self._product(o, self.out), gate_a)
+        m = ctx.norm_modulate(x, self.norm_f, scale_f, shift_f, EPS)
         h = self._product(m, self.up, epilogue="gelu_tanh")
-        return x + gate_f * self._product(h, self.down, out_dtype=torch.float32)
+        ctx.gated_residual(x, self._product(h, self.down), gate_f)
+        return x
+
+    def forward(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+        """x fp32 [S, d] (the residual stream), temb [d]: the block's output, fp32 [S, d] (x kept)."""
+        return self.forward_(x.clone(), temb)
 
     def reference(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
         """The same block in fp32 with the dequantised weights (Float(q)·s) and fp32 math attention:

@@ -281,6 +281,54 @@ class TensorGEMM:
         abi.check(st, "sq8_linear_qkv")
         return q, kk, v
 
+    # ---- the DiT block's elementwise passes ----------------------------------------------------------
+
+    def norm_modulate(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                      eps: float = 1e-6, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """bf16(((x·r)·w)·(1 + scale) + shift), r = 1/sqrt(mean(x²) + eps) per row of fp32 x
+        (`norm_modulate_rounded`, ElementwiseGPUMoss.swift:45-91)."""
+        rows, cols = x.shape
+        for t, what in ((x, "x"), (w, "w"), (scale, "scale"), (shift, "shift")):
+            if t.dtype != torch.float32:
+                raise ValueError(f"{what} must be fp32")
+        for t, what in ((w, "w"), (scale, "scale"), (shift, "shift")):
+            if t.numel() != cols or not t.is_contiguous():
+                raise ValueError(f"{what} must be {cols} contiguous values")
+        if out is None:
+            out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
+        st = abi.load().sq8_norm_modulate(self._h, _dev(x, "x"), _row_major(x, "x"), _dev(w, "w"), _dev(scale, "scale"),
+                                          _dev(shift, "shift"), float(eps), _dev(out, "out"), _row_major(out, "out"),
+                                          rows, cols)
+        abi.check(st, "sq8_norm_modulate")
+        return out
+
+    def rms_rows(self, t: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+        """In place: each row of the bf16 tensor t (last dimension ≤ 256, rows contiguous) →
+        bf16((t·r)·w) — the per-head RMSNorm of q and k."""
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError("t must be bf16 with contiguous rows")
+        cols = t.shape[-1]
+        rows = t.numel() // cols
+        ld = t.stride(-2) if t.dim() > 1 else cols
+        if t.dim() > 2 and not t.is_contiguous():
+            raise ValueError("t must be contiguous beyond its rows")
+        if w.dtype != torch.float32 or w.numel() != cols:
+            raise ValueError(f"w must be {cols} fp32 values")
+        abi.check(abi.load().sq8_rms_rows(self._h, _dev(t, "t"), ld, rows, cols, _dev(w, "w"), float(eps)), "sq8_rms_rows")
+        return t
+
+    def gated_residual(self, x: torch.Tensor, y: torch.Tensor, gate: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """In place: x += gate ⊙ y (x fp32 [rows, cols], y bf16 or fp32, gate fp32 [cols])."""
+        if x.dtype != torch.float32 or x.shape != y.shape:
+            raise ValueError("x must be fp32 and y of its shape")
+        rows, cols = x.shape
+        if gate is not None and (gate.dtype != torch.float32 or gate.numel() != cols or not gate.is_contiguous()):
+            raise ValueError(f"gate must be {cols} contiguous fp32 values")
+        st = abi.load().sq8_gated_residual(self._h, _dev(x, "x"), _row_major(x, "x"), _dev(y, "y"), _adtype(y),
+                                           _row_major(y, "y"), None if gate is None else _dev(gate, "gate"), rows, cols)
+        abi.check(st, "sq8_gated_residual")
+        return x
+
     def dequantize(self, codes: torch.Tensor, scale: Optional[torch.Tensor] = None, *,
                    layout: int = abi.SCALE_COLUMNS, block_rows: int = 0, first_row: int = 0,
                    fp8: Optional[bool] = None) -> torch.Tensor:

@@ -29,3 +29,42 @@ def test_block_flops():
     blk = DiTBlock(d=256, heads=2, mlp=4, seed=0)
     S, d = 100, 256
     assert blk.flops(S) == 2.0 * (6 * d * d + S * 12 * d * d) + 4.0 * S * S * d
+
+
+def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    return int((ia - ib).abs().max())
+
+
+def test_elementwise_passes_match_fp32():
+    # The passes against torch fp32 with the same rounding steps: the sums of squares differ only in
+    # order, so at most one bf16 unit in the last place apart.
+    from siliconed_amd import context
+    ctx = context(0)
+    g = torch.Generator(device="cuda:0").manual_seed(3)
+    S, d, hd = 300, 3072, 128
+    x = torch.randn((S, d), device="cuda:0", generator=g) * 3
+    w, sc, sh = (torch.randn(d, device="cuda:0", generator=g) * 0.1 + 1, torch.randn(d, device="cuda:0", generator=g) * 0.2,
+                 torch.randn(d, device="cuda:0", generator=g) * 0.2)
+    got = ctx.norm_modulate(x, w, sc, sh, 1e-6).double()
+    # Against float64: the final bf16 rounding (half a unit of the result: 2^(e-8) for |y| in
+    # [2^e, 2^(e+1)), at most 2^-8·|y|) plus a few fp32 units of the terms (the sum of squares in
+    # another order; v·(1 + scale) and shift can cancel).
+    x64, w64, sc64, sh64 = x.double(), w.double(), sc.double(), sh.double()
+    v = x64 / torch.sqrt((x64 * x64).mean(dim=1, keepdim=True) + 1e-6) * w64 * (sc64 + 1.0)
+    want = v + sh64
+    bound = 2.0 ** -8 * want.abs() + 2.0 ** -21 * (v.abs() + sh64.abs())
+    assert bool(((got - want).abs() <= bound).all()), float(((got - want).abs() / bound).max())
+    t = (torch.randn((S * 24, hd), device="cuda:0", generator=g) * 2).to(torch.bfloat16)
+    wt = torch.randn(hd, device="cuda:0", generator=g) * 0.1 + 1
+    t32 = t.float()
+    want = ((t32 * (1.0 / torch.sqrt((t32 * t32).mean(dim=1, keepdim=True) + 1e-6))) * wt).to(torch.bfloat16)
+    ctx.rms_rows(t, wt, 1e-6)
+    assert _bf16_ulps(t, want) <= 1
+    y = torch.randn((S, d), device="cuda:0", generator=g).to(torch.bfloat16)
+    gate = torch.randn(d, device="cuda:0", generator=g)
+    x0 = x.clone()
+    ctx.gated_residual(x, y, gate)
+    assert torch.equal(x, x0 + gate * y.float())  # one product, one sum: the same rounding
+    torch.cuda.synchronize()

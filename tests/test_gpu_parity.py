@@ -405,3 +405,28 @@ def test_skinny_glu_and_qkv(gemm, orc, tile_knob, epi):
     full = np.concatenate([t.permute(1, 0, 2).reshape(40, d).cpu().numpy() for t in (qo, ko, vo)], axis=1)
     judge(orc, full, x, q, False, s, b, "none", torch.float32)
 
+
+
+# ---- the epilogue's rounding, bit for bit -----------------------------------------------------------
+
+@pytest.mark.parametrize("m", [16, 600, 2048], ids=["skinny", "main-small", "main"])
+@pytest.mark.parametrize("layout", ["packed", "kn", "nk"])
+def test_epilogue_rounds_scale_then_bias(gemm, orc, m, layout):
+    # Integer activations and codes make every fp32 sum exact whatever its order (|sum| ≤ 3·5·3072 <
+    # 2^24), so the output must be the reference's two roundings bit for bit: the scale after the sum
+    # (TensorGEMM.swift:175-179), then the bias (Ops.swift:400-407) — not one fused multiply-add.
+    k, n = 3072, 1024
+    rng = np.random.default_rng(m)
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    q = rng.integers(-5, 6, size=(n, k)).astype(np.int8)
+    s = orc.uniform_f32(m + 1, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(m + 2, (n,), 0.0, 0.02)
+    sums = (a.astype(np.float64) @ q.astype(np.float64).T).astype(np.float32)
+    want = (sums * s) + b  # numpy float32: each operation rounded
+    x = torch.from_numpy(a).to(torch.bfloat16).to(DEV)
+    w = weight_tensor(q.view(np.uint8), False, "nk" if layout == "nk" else "kn")
+    if layout == "packed":
+        w = gemm.pack(w, layout="kn")
+    y = gemm.product(x, w, dev(s), layout="nk" if layout == "nk" else "kn", bias=dev(b), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), want)
