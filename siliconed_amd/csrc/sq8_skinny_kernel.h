@@ -8,7 +8,7 @@
 // Tile BM × 64 (one 64-column weight slab; GLU: 32 output columns, both halves), BM = 32 or 64, and
 // the K steps split over the workgroup's NWK waves: wave w takes steps w, w + NWK, w + 2·NWK, …
 // Every wave streams its steps' codes and activation fragments straight from global memory into
-// registers (two steps in flight), widens the codes there and feeds the MFMAs: no LDS and no
+// registers (PF steps in flight), widens the codes there and feeds the MFMAs: no LDS and no
 // barrier in the K loop, so the waves run independently. The NWK partial sums then meet in LDS and
 // are added in wave order (deterministic), one wave per 32 × 32 block, which runs the epilogue.
 //
@@ -22,7 +22,7 @@
 namespace sq8 {
 namespace wd {
 
-template <int BM, int NWK, int WT, int WL, int EPI, int OUT>
+template <int BM, int NWK, int PF, int WT, int WL, int EPI, int OUT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NWK, 64 * NWK), amdgpu_waves_per_eu(2, 2)))
 gemm_skinny_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -56,8 +56,8 @@ gemm_skinny_kernel(const GemmArgs p) {
     for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, j, lane);
     const uint32_t w_step = WL == W_PACKED ? 4096 : BK;
 
-    u32x4 ra[2][FM][4];  // [buffer][bm][ks]: 8 bf16 of the activation each
-    u32x4 rw[2][4];      // [buffer][load j]: 16 codes each
+    u32x4 ra[PF][FM][4];  // [buffer][bm][ks]: 8 bf16 of the activation each
+    u32x4 rw[PF][4];      // [buffer][load j]: 16 codes each
     // The loads of this wave's i-th step (clamped to the last step: prefetches past the wave's
     // last step are never used).
     auto issue = [&](int i, auto buf) {
@@ -105,16 +105,19 @@ gemm_skinny_kernel(const GemmArgs p) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     const int n = wave < KT ? (KT - wave + NWK - 1) / NWK : 0;  // this wave's steps
-    issue(0, I0{});
-    issue(1, I1{});
+    // PF steps in flight: step i in buffer i % PF, its buffer refilled with step i + PF once used.
+    static_for<0, PF>([&](auto bc) { issue(decltype(bc)::value, bc); });
     int i = 0;
-    for (; i + 1 < n; i += 2) {
-        compute(I0{});
-        issue(i + 2, I0{});
-        compute(I1{});
-        issue(i + 3, I1{});
+    for (; i + PF - 1 < n; i += PF) {
+        static_for<0, PF>([&](auto bc) {
+            constexpr int B = decltype(bc)::value;
+            compute(bc);
+            issue(i + B + PF, bc);
+        });
     }
-    if (i < n) compute(I0{});
+    static_for<0, PF - 1>([&](auto bc) {
+        if (i + decltype(bc)::value < n) compute(bc);
+    });
 
     // ---- reduction: partial sums to LDS, [wave][block][register][lane], then block e summed by
     // wave e % NWK in wave order ---------------------------------------------------------------------
@@ -179,7 +182,7 @@ gemm_skinny_kernel(const GemmArgs p) {
     }
 }
 
-template <int BM, int NWK, int WT, int WL, int EPI, int OUT>
+template <int BM, int NWK, int PF, int WT, int WL, int EPI, int OUT>
 hipError_t launch_skinny(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
@@ -188,14 +191,14 @@ hipError_t launch_skinny(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_skinny_kernel<BM, NWK, WT, WL, EPI, OUT>), dim3(blocks), dim3(64 * NWK), 0, stream, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<BM, NWK, PF, WT, WL, EPI, OUT>), dim3(blocks), dim3(64 * NWK), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int BM, int NWK, int WT, int WL>
+template <int BM, int NWK, int PF, int WT, int WL>
 hipError_t dispatch_skinny(const GemmArgs &p, int epi, int out, hipStream_t stream) {
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_skinny<BM, NWK, WT, WL, E, O>(p, stream);
+    if (epi == E && out == O) return launch_skinny<BM, NWK, PF, WT, WL, E, O>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
