@@ -163,6 +163,43 @@ int sq8_dequantize(sq8_ctx *ctx, const void *codes, int w_dtype, int64_t rows, i
  * Replaces: the `round_bf16` pass (TensorGEMMBF16.swift:41-48, 67-73). */
 int sq8_round_bf16(sq8_ctx *ctx, const float *x, uint16_t *y, int64_t count);
 
+/* ---- ComfyUI's int8 convrot: the weight published rotated, W = (q·s)·R, R = H/√G block-diagonal
+ * along the input, G ∈ {4, 16, 64, 256}, H the Kronecker power of the regular Hadamard
+ * H4 = [[1,1,1,−1],[1,1,−1,1],[1,−1,1,1],[−1,1,1,1]] (Sources/Siliconed/Widen.swift:316-343).
+ * A group that is not one of those, or k not a multiple of it, is SQ8_EINVAL (the reference's
+ * precondition, Widen.swift:381). ---- */
+
+/* **The product of a rotated weight**: `sq8_linear` on the activation rotated first, C = act(s ⊙
+ * ((A·R) · q) + b), A·R computed in fp32 by the reference's butterflies then rounded to bf16 once
+ * (A fp32 or bf16), into the context's scratch. Replaces: TensorGEMM.linear(…rotation:…) with
+ * `rotation` set (TensorGEMM.swift:264-290), i.e. submitRounded's rotate_groups → round_bf16 →
+ * product (TensorGEMMBF16.swift:208-264) and submit's rotate_groups → product (TensorGEMM.swift:335-346). */
+int sq8_linear_rotated(sq8_ctx *ctx,
+                       const void *a, int a_dtype, int64_t lda, int group,
+                       const void *w, int w_dtype, int w_layout, int64_t ldw,
+                       const float *scale, int scale_layout,
+                       const float *bias, int epilogue,
+                       void *c, int c_dtype, int64_t ldc,
+                       int m, int k, int n, double *gpu_seconds);
+
+/* **The activation's rotation**: y = x·R for `rows` rows of k values; x SQ8_F32 or SQ8_BF16 (leading
+ * dimension ldx), y SQ8_F32 or SQ8_BF16 (rounded to nearest even; ldy). fp32 butterflies in the
+ * reference's stage order (spans 1, 4, 16, 64), then × 1/√G. y may be x itself (same type and
+ * leading dimension), no other overlap. Replaces: `rotate_groups` (TensorGEMM.swift:181-201) and,
+ * with a bf16 y, the `round_bf16` after it (TensorGEMMBF16.swift:222-233); the rotation once per
+ * input for several products on it (DecodeKernels.swift:19-21). */
+int sq8_rotate_groups(sq8_ctx *ctx, const void *x, int x_dtype, int64_t ldx, void *y, int y_dtype, int64_t ldy,
+                      int rows, int k, int group);
+
+/* **The rotated weight widened**: out[r, c] = Float(m) · (s_c · 1/√G), m = H·q over each group of
+ * `group` rows of column c (exact integers), for int8 codes [k, n] (leading dimension ldq) rotated
+ * along k; scale SQ8_F32/SQ8_BF16/SQ8_F16, one per column (SQ8_SCALE_COLUMNS) or one
+ * (SQ8_SCALE_TENSOR); out fp32 [k, n] (leading dimension ldo). A slice of columns is the same call
+ * on codes + first, scale + first, with n = the slice's width. Replaces: Widen.dequantizeRotated
+ * (Widen.swift:374-428), as reached from Artifact.materialize (Artifact.swift:694-706). */
+int sq8_dequantize_rotated(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, int k, int n, int group,
+                           const void *scale, int scale_dtype, int scale_layout, float *out, int64_t ldo);
+
 /* ---- the elementwise passes of a DiT block around the products (all device pointers, queued) ---- */
 
 /* **Modulated RMSNorm to the next product's operand**: for each of `rows` rows of fp32 x (leading

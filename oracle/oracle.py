@@ -56,6 +56,10 @@ def _declare(l: ctypes.CDLL) -> None:
         "orc_f32_to_e4m3": (ctypes.c_uint8, [ctypes.c_float]),
         "orc_quantize_e4m3": (None, [P, P, SZ]),
         "orc_dequantize": (None, [P, I, SZ, P, I, I, SZ, SZ, SZ, P]),
+        "orc_is_rotation_group": (I, [I]),
+        "orc_rotation_norm": (ctypes.c_float, [I]),
+        "orc_rotate_groups": (None, [P, I64, P, I64, I, I, I]),
+        "orc_dequantize_rotated": (None, [P, I64, I, I, I, P, I, I, P, I64]),
         "orc_gelu_tanh": (D, [D]),
         "orc_silu_glu": (D, [D, D]),
         "orc_situ": (D, [D, D]),
@@ -163,6 +167,35 @@ def dequantize(values: np.ndarray, kind: int, scale: np.ndarray | None, scale_ty
     lib().orc_dequantize(_p(values), kind, values.size, _p(sc), scale_type, layout, columns, block_rows,
                          first_row, _p(out))
     return out.reshape(values.shape)
+
+
+# ---- convrot: Sources/Siliconed/Widen.swift:316-428, TensorGEMM.swift:181-201 -------------
+
+def is_rotation_group(g: int) -> bool:
+    """Widen.swift:335-340: a power of 4, 4 to 256."""
+    return bool(lib().orc_is_rotation_group(int(g)))
+
+
+def rotate_groups(x: np.ndarray, group: int) -> np.ndarray:
+    """TensorGEMM.swift:183-201: fp32 rows [rows, k] times R = H/sqrt(G) by groups (fp32 butterflies)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    assert k % group == 0 and is_rotation_group(group)
+    y = np.empty_like(x)
+    lib().orc_rotate_groups(_p(x), k, _p(y), k, rows, k, group)
+    return y
+
+
+def dequantize_rotated(q: np.ndarray, group: int, scale: np.ndarray, scale_type: int = F32,
+                       layout: int = SCALE_COLUMNS) -> np.ndarray:
+    """Widen.swift:374-428: int8 [k, n] -> fp32 Float(H.q) * (s / sqrt(G)) per group of rows."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    k, n = q.shape
+    assert k % group == 0 and is_rotation_group(group)
+    out = np.empty((k, n), dtype=np.float32)
+    sc = np.ascontiguousarray(scale)
+    lib().orc_dequantize_rotated(_p(q), n, k, n, group, _p(sc), scale_type, layout, _p(out), n)
+    return out
 
 
 # ---- truth and judgement ------------------------------------------------------------------

@@ -201,6 +201,76 @@ void orc_dequantize(const void *values, int kind, size_t count, const void *scal
 }
 
 /* ---------------------------------------------------------------------------------------------
+ * ComfyUI's convrot: Sources/Siliconed/Widen.swift:316-428 and the activation's rotation
+ * Sources/Siliconed/TensorGEMM.swift:181-201.
+ * ------------------------------------------------------------------------------------------- */
+int orc_is_rotation_group(int g) {
+    /* Widen.isRotationGroup (Widen.swift:335-340): a power of 4 from 4 to 256. */
+    int p = 4;
+    while (p < g) p *= 4;
+    return p == g && g <= 256;
+}
+
+float orc_rotation_norm(int g) {
+    /* Widen.rotationNorm (Widen.swift:343): 1 / √G, a power of two for a power of 4. */
+    return 1.0f / sqrtf((float)g);
+}
+
+void orc_rotate_groups(const float *x, int64_t ldx, float *y, int64_t ldy, int rows, int k, int group) {
+    /* rotate_groups (TensorGEMM.swift:183-201), one group at a time: spans 1, 4, 16, 64 below G;
+     * the 4-point butterfly p = a + b, m = a − b, u = c + d, w = c − d → (p + w, p − w, m + u, u − m),
+     * every sum rounded to fp32 on its own; then each value times 1/√G. */
+    const float norm = orc_rotation_norm(group);
+#pragma omp parallel for schedule(static) if ((int64_t)rows * k > (1L << 18))
+    for (int r = 0; r < rows; ++r) {
+        float v[256];
+        for (int g0 = 0; g0 < k; g0 += group) {
+            for (int i = 0; i < group; ++i) v[i] = x[(int64_t)r * ldx + g0 + i];
+            for (int span = 1; span < group; span *= 4) {
+                for (int t = 0; t < group / 4; ++t) {
+                    const int j = (t / span) * 4 * span + t % span;
+                    const float a = v[j], b = v[j + span], c = v[j + 2 * span], d = v[j + 3 * span];
+                    const float p = a + b, m = a - b, u = c + d, w = c - d;
+                    v[j] = p + w;
+                    v[j + span] = p - w;
+                    v[j + 2 * span] = m + u;
+                    v[j + 3 * span] = u - m;
+                }
+            }
+            for (int i = 0; i < group; ++i) y[(int64_t)r * ldy + g0 + i] = v[i] * norm;
+        }
+    }
+}
+
+void orc_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int group, const void *scale,
+                            int scale_type, int layout, float *out, int64_t ldo) {
+    /* Widen.dequantizeRotated (Widen.swift:374-428): per column c and group of G rows, the integer
+     * m = H·q (H the unnormalized Kronecker power of H4, exact in int32: |m| ≤ 32 648 for G = 256),
+     * then out = Float(m) · f_c with f_c = s_c · (1/√G) (one fp32 multiply each). Scales per column
+     * (layout COLUMNS, n of them) or one for the tensor (TENSOR). */
+    const float norm = orc_rotation_norm(group);
+#pragma omp parallel for schedule(static) if ((int64_t)k * n > (1L << 18))
+    for (int c = 0; c < n; ++c) {
+        const float f = scale_value(scale, scale_type, layout == ORC_SCALE_TENSOR ? 0 : (size_t)c) * norm;
+        int32_t v[256];
+        for (int g0 = 0; g0 < k; g0 += group) {
+            for (int i = 0; i < group; ++i) v[i] = q[(int64_t)(g0 + i) * ldq + c];
+            for (int span = 1; span < group; span *= 4) {
+                for (int t = 0; t < group / 4; ++t) {
+                    const int j = (t / span) * 4 * span + t % span;
+                    const int32_t a = v[j], b = v[j + span], cc = v[j + 2 * span], d = v[j + 3 * span];
+                    v[j] = a + b + cc - d;
+                    v[j + span] = a + b - cc + d;
+                    v[j + 2 * span] = a - b + cc + d;
+                    v[j + 3 * span] = -a + b + cc + d;
+                }
+            }
+            for (int i = 0; i < group; ++i) out[(int64_t)(g0 + i) * ldo + c] = (float)v[i] * f;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------
  * Epilogues in double.
  * ------------------------------------------------------------------------------------------- */
 double orc_gelu_tanh(double x) {

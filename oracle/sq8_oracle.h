@@ -54,6 +54,21 @@ void orc_quantize_e4m3(const float *x, uint8_t *out, size_t count);
 void orc_dequantize(const void *values, int kind, size_t count, const void *scale, int scale_type,
                     int layout, size_t columns, size_t block_rows, size_t first_row, float *out);
 
+/* ---- ComfyUI's convrot (int8_tensorwise with a Hadamard rotation of the input) ---- */
+/* Widen.isRotationGroup (Sources/Siliconed/Widen.swift:335-340): a power of 4, 4 to 256. */
+int orc_is_rotation_group(int g);
+/* 1/√G (Widen.swift:343). */
+float orc_rotation_norm(int g);
+/* y = x·R along each of `rows` rows of k values (k a multiple of `group`), R = H/√G block-diagonal:
+ * the radix-4 butterflies of rotate_groups (Sources/Siliconed/TensorGEMM.swift:183-201) in fp32,
+ * stage order and sums as there, then × 1/√G. x and y may not overlap. */
+void orc_rotate_groups(const float *x, int64_t ldx, float *y, int64_t ldy, int rows, int k, int group);
+/* Widen.dequantizeRotated (Widen.swift:374-428): codes q [k, n] (leading dimension ldq), rotated
+ * along k by groups of `group` rows, exact integers H·q, then Float(m) · (s · 1/√G); scale of type
+ * `scale_type` (F32/BF16/F16), one per column (COLUMNS) or one (TENSOR). out [k, n], leading ldo. */
+void orc_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int group, const void *scale,
+                            int scale_type, int layout, float *out, int64_t ldo);
+
 /* ---- epilogues, in double (the definitions the GPU is judged against) ---- */
 /* nn.GELU(approximate="tanh") in double: Sources/Siliconed/QwenImage21.swift:953-963. */
 double orc_gelu_tanh(double x);

@@ -32,6 +32,7 @@ SOURCES = [
     ("sq8_wdirect_inst.hip", "sq8_wdirect_f8_packed", ["-DSQ8_WT=1", "-DSQ8_WL=2"]),
     ("sq8_aux.hip", "sq8_aux", []),
     ("sq8_block.hip", "sq8_block", []),
+    ("sq8_convrot.hip", "sq8_convrot", []),
     ("sq8_api.hip", "sq8_api", []),
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -97,6 +97,7 @@ struct Product {
     const float *scale; int scale_layout; const float *bias; int epilogue;
     void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
     int m, k, n;
+    int group;  // convrot: the operand rotated by groups of `group` first (0: none)
 };
 
 int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
@@ -112,6 +113,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (q.lda < q.k) return SQ8_EINVAL;
     if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
+    if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
 
     DeviceScope scope(ctx->device);
     if (scope.error != hipSuccess) return hip_status(scope.error);
@@ -124,7 +126,19 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
     }
-    if (q.a_dtype == SQ8_F32) {
+    if (q.group != 0) {
+        // convrot: the operand rotated (fp32 butterflies) and rounded to bf16 in one pass, into the
+        // context's scratch (TensorGEMMBF16.swift:222-233: rotate_groups, then round_bf16).
+        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
+        if (st != SQ8_OK) return st;
+        uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
+        hipError_t e = sq8::launch_rotate_groups(q.a, q.a_dtype == SQ8_BF16, q.lda, y, true, q.k, q.m, q.k, q.group,
+                                                 ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        p.a = y;
+        p.lda = q.k;
+    } else if (q.a_dtype == SQ8_F32) {
         // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
         const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
         st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
@@ -334,6 +348,49 @@ int sq8_linear_qkv(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const 
     q.split = d; q.head_dim = head_dim;
     q.m = m; q.k = k; q.n = 3 * d;
     return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_rotated(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group, const void *w, int w_dtype,
+                       int w_layout, int64_t ldw, const float *scale, int scale_layout, const float *bias, int epilogue,
+                       void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    if (group == 0) return SQ8_EINVAL;
+    Product q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda; q.group = group;
+    q.w = w; q.w_dtype = w_dtype; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_rotate_groups(sq8_ctx *ctx, const void *x, int x_dtype, int64_t ldx, void *y, int y_dtype, int64_t ldy, int rows,
+                      int k, int group) {
+    if (!ctx || rows < 0 || k < 0) return SQ8_EINVAL;
+    if ((x_dtype != SQ8_F32 && x_dtype != SQ8_BF16) || (y_dtype != SQ8_F32 && y_dtype != SQ8_BF16)) return SQ8_EUNSUPPORTED;
+    if (!sq8::is_rotation_group(group) || k % group != 0) return SQ8_EINVAL;
+    if (rows == 0 || k == 0) return SQ8_OK;
+    if (!x || !y || ldx < k || ldy < k) return SQ8_EINVAL;
+    // In place only as the same buffer read and written alike: each chunk is read whole before it is written.
+    if (x == y && (x_dtype != y_dtype || ldx != ldy)) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_rotate_groups(x, x_dtype == SQ8_BF16, ldx, y, y_dtype == SQ8_BF16, ldy, rows, k, group,
+                                                ctx->stream));
+}
+
+int sq8_dequantize_rotated(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, int k, int n, int group, const void *scale,
+                           int scale_dtype, int scale_layout, float *out, int64_t ldo) {
+    if (!ctx || k < 0 || n < 0) return SQ8_EINVAL;
+    if (scale_dtype != SQ8_F32 && scale_dtype != SQ8_BF16 && scale_dtype != SQ8_F16) return SQ8_EUNSUPPORTED;
+    if (scale_layout != SQ8_SCALE_TENSOR && scale_layout != SQ8_SCALE_COLUMNS) return SQ8_EUNSUPPORTED;
+    if (!sq8::is_rotation_group(group) || k % group != 0) return SQ8_EINVAL;
+    if (k == 0 || n == 0) return SQ8_OK;
+    if (!codes || !scale || !out || ldq < n || ldo < n) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_dequantize_rotated(codes, ldq, k, n, group, scale, scale_dtype,
+                                                     scale_layout == SQ8_SCALE_COLUMNS, out, ldo, ctx->stream));
 }
 
 int64_t sq8_packed_bytes(int k, int n, int glu) {

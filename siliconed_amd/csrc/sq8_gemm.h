@@ -65,6 +65,15 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
                              hipStream_t stream);
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
 
+// ComfyUI's convrot (sq8_convrot.hip): the activation's rotation x·R by groups of `group` (4, 16,
+// 64 or 256; k a multiple of it), fp32 or bf16 in, fp32 or bf16 (rounded to nearest even) out; and
+// the rotated weight widened, Float(H·q)·(s/√G), codes [k, n] rotated along k.
+bool is_rotation_group(int group);
+hipError_t launch_rotate_groups(const void *x, bool x_bf16, int64_t ldx, void *y, bool y_bf16, int64_t ldy, int64_t rows,
+                                int k, int group, hipStream_t stream);
+hipError_t launch_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int group, const void *scale,
+                                     int scale_dtype, bool per_column, float *out, int64_t ldo, hipStream_t stream);
+
 // The DiT block's elementwise passes (sq8_block.hip).
 hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,
                                 float eps, uint16_t *out, int64_t ldo, int rows, int cols, hipStream_t stream);

@@ -140,16 +140,18 @@ class TensorGEMM:
         map's) at `weight_offset` bytes into `int8`, its fp32 scales at `scales_offset` bytes into
         `scales` (`n` of them, or one: `per_column` False). `a` fp32 is rounded to bf16 first when
         `rounding` (the `rounding:` scratch route, TensorGEMMBF16.swift:208-264); `a` bf16 is
-        already rounded. Returns the GPU seconds, 0 when `settled` (queued).
+        already rounded. `rotation`: a convrot weight's group (an int, or the reference's
+        `(group, scratch, offset, chunk)`, whose scratch and chunk this library replaces with its
+        own), the activation rotated by it first (TensorGEMMBF16.swift:222-233). Returns the GPU
+        seconds, 0 when `settled` (queued).
 
         Routes this library does not take raise `abi.Unsupported` before any work, as the
         reference's `nil` pipelines send the caller back to the widened route: Q8_0 `block`
-        scales, convrot `rotation`, W8A8 `quantizing`, an fp32 activation not rounded.
+        scales, W8A8 `quantizing`, an fp32 activation not rounded.
         """
         if block is not None:
             raise abi.Unsupported(abi.EUNSUPPORTED, "Q8_0 block scales")
-        if rotation is not None:
-            raise abi.Unsupported(abi.EUNSUPPORTED, "convrot rotation")
+        group = 0 if rotation is None else int(rotation[0] if isinstance(rotation, (tuple, list)) else rotation)
         if quantizing is not None:
             raise abi.Unsupported(abi.EUNSUPPORTED, "W8A8 activation quantization")
         if a.dtype == torch.float32 and not rounding:
@@ -168,14 +170,14 @@ class TensorGEMM:
             raise ValueError("the scales' offset must be a multiple of 4 bytes")
         ldw = n if lay == abi.KN else k
         secs = ctypes.c_double(0.0)
-        st = abi.load().sq8_linear(
-            self._h, _dev(a, "a"), _adtype(a), k,
-            _dev(int8, "int8") + weight_offset, wd, lay, ldw,
-            _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
-            None if bias is None else _dev(bias, "bias"), epi,
-            _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
-            None if settled else ctypes.byref(secs))
-        abi.check(st, "sq8_linear")
+        args = ((self._h, _dev(a, "a"), _adtype(a), k) + ((group,) if group else ()) +
+                (_dev(int8, "int8") + weight_offset, wd, lay, ldw,
+                 _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
+                 None if bias is None else _dev(bias, "bias"), epi,
+                 _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                 None if settled else ctypes.byref(secs)))
+        name = "sq8_linear_rotated" if group else "sq8_linear"
+        abi.check(getattr(abi.load(), name)(*args), name)
         return 0.0 if settled else secs.value
 
     # ---- staging -----------------------------------------------------------------------------
@@ -202,9 +204,10 @@ class TensorGEMM:
     def product(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
                 bias: Optional[torch.Tensor] = None, epilogue=None, out: Optional[torch.Tensor] = None,
                 out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None,
-                timed: bool = False):
+                timed: bool = False, rotation: int = 0):
         """y = act(s ⊙ (x · Wᵀ) + b) for x [m, k] and W [n, k] (`layout="nk"`, nn.Linear) or
-        [k, n] (`"kn"`, the map's). Returns y (and the GPU seconds when `timed`)."""
+        [k, n] (`"kn"`, the map's). `rotation` = G: a convrot weight, x rotated by groups of G
+        first (y = act(s ⊙ ((x·R) · qᵀ) + b)). Returns y (and the GPU seconds when `timed`)."""
         epi = _epilogue(epilogue)
         m, k = x.shape
         if isinstance(w, PackedWeight):
@@ -236,14 +239,14 @@ class TensorGEMM:
         elif tuple(out.shape) != (m, n_out):
             raise ValueError("out has the wrong shape")
         secs = ctypes.c_double(0.0)
-        st = abi.load().sq8_linear(
-            self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
-            wptr, wd, lay, ldw,
-            _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
-            None if bias is None else _dev(bias, "bias"), epi,
-            _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
-            ctypes.byref(secs) if timed else None)
-        abi.check(st, "sq8_linear")
+        args = ((self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x")) + ((int(rotation),) if rotation else ()) +
+                (wptr, wd, lay, ldw,
+                 _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
+                 None if bias is None else _dev(bias, "bias"), epi,
+                 _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+                 ctypes.byref(secs) if timed else None))
+        name = "sq8_linear_rotated" if rotation else "sq8_linear"
+        abi.check(getattr(abi.load(), name)(*args), name)
         return (out, secs.value) if timed else out
 
     def product_qkv(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
@@ -350,6 +353,43 @@ class TensorGEMM:
         abi.check(st, "sq8_dequantize")
         return out.reshape(codes.shape)
 
+    def rotate(self, x: torch.Tensor, group: int, *, out: Optional[torch.Tensor] = None,
+               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """x·R by groups of `group` along the rows of x [rows, k] (fp32 or bf16): the activation's
+        convrot rotation (rotate_groups, TensorGEMM.swift:181-201), fp32 butterflies, the result
+        rounded to bf16 (`out_dtype`) or kept fp32. `out` may be x itself (same dtype)."""
+        if x.dim() != 2:
+            raise ValueError("x must be 2-D [rows, k]")
+        rows, k = x.shape
+        if out is None:
+            out = torch.empty((rows, k), dtype=out_dtype, device=x.device)
+        elif tuple(out.shape) != (rows, k):
+            raise ValueError("out has the wrong shape")
+        st = abi.load().sq8_rotate_groups(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"),
+                                          _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), rows, k,
+                                          int(group))
+        abi.check(st, "sq8_rotate_groups")
+        return out
+
+    def dequantize_rotated(self, codes: torch.Tensor, group: int, scale: torch.Tensor) -> torch.Tensor:
+        """Float(H·q)·(s/√G) of int8 codes [k, n] rotated along k (Widen.dequantizeRotated,
+        Widen.swift:374-428): fp32 [k, n]. `scale` fp32/bf16/fp16, n of them or one."""
+        if codes.dtype != torch.int8 or codes.dim() != 2:
+            raise ValueError("codes must be int8 [k, n]")
+        k, n = codes.shape
+        sd = {torch.float32: abi.F32, torch.bfloat16: abi.BF16, torch.float16: abi.F16}.get(scale.dtype)
+        if sd is None:
+            raise ValueError("scales are fp32, bf16 or fp16")
+        if scale.numel() not in (1, n):
+            raise ValueError("scale: n of them, or one")
+        out = torch.empty((k, n), dtype=torch.float32, device=codes.device)
+        st = abi.load().sq8_dequantize_rotated(self._h, _dev(codes, "codes"), _row_major(codes, "codes"), k, n,
+                                               int(group), _dev(scale, "scale"), sd,
+                                               abi.SCALE_COLUMNS if scale.numel() == n and n != 1 else abi.SCALE_TENSOR,
+                                               _dev(out, "out"), n)
+        abi.check(st, "sq8_dequantize_rotated")
+        return out
+
     def round_bf16(self, x: torch.Tensor) -> torch.Tensor:
         """fp32 → bf16 nearest-even (TensorGEMMBF16.swift:41-48)."""
         if x.dtype != torch.float32 or not x.is_contiguous():
@@ -392,6 +432,14 @@ def pack(w, **kw):
 
 def dequantize(codes, scale=None, **kw):
     return context(codes.device.index).dequantize(codes, scale, **kw)
+
+
+def rotate(x, group, **kw):
+    return context(x.device.index).rotate(x, group, **kw)
+
+
+def dequantize_rotated(codes, group, scale):
+    return context(codes.device.index).dequantize_rotated(codes, group, scale)
 
 
 def round_bf16(x):

@@ -265,3 +265,119 @@ def test_linear_f32_is_the_fp32_product(orc, epi):
     p = orc.bf16_to_f32(a) @ w_kn
     ref = orc.epilogue_f32(p, bias=b, epilogue=e, threads=2)
     np.testing.assert_allclose(c, ref, rtol=2e-4, atol=2e-5)
+
+
+# ---- convrot: Sources/Siliconed/Widen.swift:316-428, TensorGEMM.swift:181-201 ----------------------
+
+H4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+
+
+def hadamard(g: int) -> np.ndarray:
+    """The unnormalized rotation of a group, built independently of the oracle's butterflies: the
+    Kronecker power of the regular H4 (Widen.swift:319-323)."""
+    h = np.ones((1, 1))
+    while h.shape[0] < g:
+        h = np.kron(h, H4)
+    return h
+
+
+def test_rotation_groups_and_the_matrix(orc):
+    # A power of 4 from 4 to 256, nothing else; H symmetric with H·H = G·I (R = H/√G orthogonal).
+    assert [g for g in range(0, 1100) if orc.is_rotation_group(g)] == [4, 16, 64, 256]
+    for g in (4, 16, 64, 256):
+        h = hadamard(g)
+        assert np.array_equal(h, h.T) and np.array_equal(h @ h, g * np.eye(g))
+        assert float(orc.lib().orc_rotation_norm(g)) == 1 / math.sqrt(g)
+
+
+def _bf16_scales(orc, n, rng):
+    s = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    b = orc.f32_to_bf16(s)
+    return b, orc.bf16_to_f32(b)
+
+
+@pytest.mark.parametrize("g,k,n", [(256, 768, 328), (256, 256, 12), (64, 192, 136), (16, 64, 40), (4, 8, 20),
+                                   (16, 32, 8200), (4, 8, 4100)])
+def test_dequantize_rotated_is_the_exact_hadamard_product(orc, g, k, n):
+    # DequantizeTests.swift:179-211, same shapes: Float(H·q)·(s/√G) at the bit, H·q as an fp64 matrix
+    # product of the Kronecker-built H (integers under 2^53: exact), the extremes of m in columns 0
+    # and 1 (±127/−128 following H's first row), bf16 and fp32 scales per column, one fp32 scale for
+    # the tensor. Catches a wrong sign or digit in the butterflies, a scale applied before the sum,
+    # a missing 1/√G, a transposed walk of the [k, n] codes.
+    rng = np.random.default_rng(g * 7 + k + n)
+    q = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    h = hadamard(g)
+    q[:g, 0] = np.where(h[0] > 0, 127, -128)
+    q[:g, 1] = np.where(h[0] > 0, -128, 127)
+    m = np.concatenate([h @ q[g0:g0 + g].astype(np.float64) for g0 in range(0, k, g)])
+    assert np.abs(m).max() <= 32648
+    norm = np.float32(1 / math.sqrt(g))
+    bits, sb = _bf16_scales(orc, n, rng)
+    sf = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    for scale, stype, layout, s32 in ((bits, orc.BF16, orc.SCALE_COLUMNS, sb), (sf, orc.F32, orc.SCALE_COLUMNS, sf),
+                                      (sf[:1], orc.F32, orc.SCALE_TENSOR, np.full(n, sf[0], np.float32))):
+        got = orc.dequantize_rotated(q, g, scale, stype, layout)
+        expected = m.astype(np.float32) * (s32 * norm)
+        assert bitwise_equal(got, expected) == 0, (g, k, n, stype, layout)
+
+
+def test_dequantize_rotated_extreme_columns_reach_the_bound(orc):
+    # H's rows sum to +16 at G = 256: 136 plus and 120 minus signs. Codes following the first row
+    # give m = 136·127 + 120·128 = 32 632; the opposite signs (−128 on the plus) give −(136·128 +
+    # 120·127) = −32 648, the Int16 bound the reference states (Widen.swift:327-329).
+    g = 256
+    h = hadamard(g)
+    assert (h[0] > 0).sum() == 136 and h.sum(axis=1).tolist() == [16.0] * g
+    q = np.zeros((g, 4), np.int8)
+    q[:, 0] = np.where(h[0] > 0, 127, -128)
+    q[:, 1] = np.where(h[0] > 0, -128, 127)
+    out = orc.dequantize_rotated(q, g, np.ones(4, np.float32) * 16, orc.F32)
+    assert out[0, 0] == 32632.0 and out[0, 1] == -32648.0
+
+
+@pytest.mark.parametrize("g", [4, 16, 64, 256])
+def test_rotate_groups_is_the_exact_product_on_integers(orc, g):
+    # Integers |x| ≤ 1024: every partial sum (≤ 2^18) is exact in fp32, so the rotation must equal
+    # x·H/√G from the Kronecker-built H whatever the order of the sums. Catches a wrong sign, a wrong
+    # span-to-digit mapping, a transposed group, a missing norm, groups that straddle rows.
+    rng = np.random.default_rng(g)
+    k = 3 * 256
+    x = rng.integers(-1024, 1025, (5, k)).astype(np.float32)
+    h = hadamard(g)
+    expected = np.concatenate([x[:, g0:g0 + g].astype(np.float64) @ h for g0 in range(0, k, g)], axis=1) / math.sqrt(g)
+    assert np.array_equal(orc.rotate_groups(x, g).astype(np.float64), expected)
+
+
+def test_rotate_groups_rounds_the_pairwise_sums(orc):
+    # Known answers worked by hand, fp32 round-to-nearest-even (ulp 2 at 2^24):
+    # (2^24, 1, −2^24, 1): p = 2^24+1 → 2^24 (tie), m = 2^24−1, u = −(2^24−1), w = −2^24−1 → −2^24;
+    #   out = (p+w, p−w, m+u, u−m)/2 = (0, 2^25, 0, −(2^25−2))/2. Left-to-right a+b+c−d gives −1 first.
+    # (2^24, 1, 1, 0): p → 2^24, m = 2^24−1, u = w = 1: p+w = 2^24+1 → 2^24 (the correctly rounded
+    #   a+b+c−d is 2^24+2), p−w = 2^24−1, m+u = 2^24, u−m = −(2^24−2).
+    T = 2.0 ** 24
+    for x, y in (((T, 1, -T, 1), (0, T, 0, -(T - 1))), ((T, 1, 1, 0), (T / 2, (T - 1) / 2, T / 2, -(T - 2) / 2))):
+        got = orc.rotate_groups(np.array([x], np.float32), 4)[0]
+        assert np.array_equal(got.astype(np.float64), np.array(y)), (x, got)
+
+
+def test_rotate_groups_runs_span_one_first(orc):
+    # G = 16, x0 = 2^24, x1 = x4 = 1 (by hand). Span 1 first: quad 0 → (2^24, 2^24, 2^24−1, −(2^24−1))
+    # (the tie drops the 1), quad 1 → (1, 1, 1, −1); then span 4 per column j: j = 2 adds 2^24−1 and
+    # 1 exactly → out[2] = 2^24. Span 4 first would give out[2] = 2^24−1. All over √16 = 4.
+    T = 2.0 ** 24
+    x = np.zeros((1, 16), np.float32)
+    x[0, 0], x[0, 1], x[0, 4] = T, 1, 1
+    y = np.array([T, T, T, -T, T, T, T, -T, T - 1, T - 1, T - 2, -(T - 2), -(T - 1), -(T - 1), -(T - 2), T - 2]) / 4
+    assert np.array_equal(orc.rotate_groups(x, 16)[0].astype(np.float64), y)
+
+
+def test_rotate_groups_is_its_own_inverse_within_rounding(orc):
+    # R = H/√G is symmetric and orthogonal: R·R = I. Two rotations give x back to within the fp32
+    # roundings of 2·log4(G) butterfly stages (each a sum of two rounded sums).
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((7, 1024)) * 3).astype(np.float32)
+    for g in (4, 16, 64, 256):
+        back = orc.rotate_groups(orc.rotate_groups(x, g), g)
+        stages = 2 * int(round(math.log(g, 4)))
+        assert np.abs(back - x).max() <= 4 * stages * 2.0 ** -24 * np.abs(x).max() * math.sqrt(g) / 4 + 1e-6
+        assert np.abs(back - x).max() > 0 or g == 4
