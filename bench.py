@@ -59,7 +59,14 @@ WORKLOADS = {
                 "C3 fp8-e4m3 down-projection [3840, 10240], bias, bf16 out"),
     "c3_plain": (4096, 3840, 12288, "fp8", None, "normal",
                  "C3 plain fp8-e4m3 linear W [12288, 3840], bias, bf16 out"),
+    "c1_convrot": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
+                   "C1 up-projection on a convrot int8 weight (groups of 256): fp32 X rotated and rounded to bf16, "
+                   "then the product with bias + fused GELU-tanh, bf16 out"),
 }
+# Workloads whose weight is ComfyUI's convrot: the rotation group. Their activation is fp32 (the
+# reference's rotate_groups reads fp32, TensorGEMM.swift:181-201) and a step is the rotation pass
+# (fp32 → bf16) followed by the product — the two kernels sq8_linear_rotated runs.
+ROTATED = {"c1_convrot": 256}
 SEEDS = {"x": 1, "w": 2, "scale": 3, "bias": 4}
 
 
@@ -110,15 +117,18 @@ def inputs(workload: str):
     return x, q, s.numpy().astype(np.float32), b
 
 
-def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0):
+def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0, x32=None):
     """The reference's CPU route on a sample of rows: the whole weight widened (oracle dequantiser,
-    every core), the sample's fp32 GEMM (numpy's BLAS, the cblas_sgemm of the reference), bias +
-    activation in fp32 (oracle). Repeated for about `budget_s`; scaled to all M rows."""
+    every core; a convrot weight with its rotation, Widen.dequantizeRotated), the sample's fp32 GEMM
+    (numpy's BLAS, the cblas_sgemm of the reference) on the bf16 activation or, for a convrot weight,
+    the fp32 one, bias + activation in fp32 (oracle). Repeated for about `budget_s`; scaled to all M
+    rows."""
     from oracle import oracle
     M, K, N, wt, epi, _, _ = WORKLOADS[workload]
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     rows = min(512, M)
-    a32 = oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
+    group = ROTATED.get(workload)
+    a32 = x32[:rows] if group else oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
     if wt == "int8":
         codes, kind = q.view(np.uint8), oracle.INT8            # [K, N], scales per column
     else:
@@ -128,7 +138,10 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0):
     start = time.perf_counter()
     while time.perf_counter() - start < budget_s or reps < 2:
         t0 = time.perf_counter()
-        w = oracle.dequantize(codes, kind, s, oracle.F32, oracle.SCALE_COLUMNS, columns=N)
+        if group:
+            w = oracle.dequantize_rotated(q, group, s)
+        else:
+            w = oracle.dequantize(codes, kind, s, oracle.F32, oracle.SCALE_COLUMNS, columns=N)
         t1 = time.perf_counter()
         y = oracle.epilogue_f32(a32 @ w.reshape(K, N), bias=b, epilogue=e, threads=threads)
         t2 = time.perf_counter()
@@ -253,7 +266,24 @@ def main() -> int:
         torch.cuda.synchronize()
         stage_ms = 1e3 * (time.perf_counter() - t_stage)
     n_out = N // 2 if glu else N
-    if qkv:
+    group = ROTATED.get(args.workload)
+    x32 = None
+    if group:
+        x32 = normal_f32(SEEDS["x"], M * K).reshape(M, K)
+        x32d = torch.from_numpy(x32).to(dev)
+        xd = torch.empty((M, K), dtype=torch.bfloat16, device=dev)   # the rotated, rounded operand
+        out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
+
+        def step(marks=None):
+            if marks:
+                marks[0].record()
+            ctx.rotate(x32d, group, out=xd)
+            if marks:
+                marks[1].record()
+            ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
+            if marks:
+                marks[2].record()
+    elif qkv:
         outs = tuple(torch.empty((M, N // 3), dtype=torch.bfloat16, device=dev) for _ in range(3))
 
         def step():
@@ -268,23 +298,39 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)] if group else None
     t0 = time.perf_counter()
     ev0.record()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        if group:
+            step(marks[i])
+        else:
+            step()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     # The events are recorded on torch's current stream, the stream the context launches on.
-    kernel_ms = ev0.elapsed_time(ev1) / args.steps
+    step_ms = ev0.elapsed_time(ev1) / args.steps
+    kernel_ms = step_ms
+    rotation = None
+    if group:
+        # The product kernel's own time (the roofline's), and the rotation pass's, from the marks
+        # around each launch; the step (value) is both.
+        kernel_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
+        rot_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
+        rot_bytes = 4 * M * K + 2 * M * K
+        rotation = {"group": group, "ms": round(rot_ms, 5), "algorithmic_bytes": rot_bytes, "bound": "hbm",
+                    "achieved": round(rot_bytes / (rot_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(rot_bytes / (rot_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     flops = 2.0 * M * N * K
-    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    tflops = flops / (step_ms * 1e-3) / 1e12
+    kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
     algo_bytes = 2 * M * K + N * K + 4 * N + 4 * N + 2 * M * n_out
     intensity = flops / algo_bytes
     gbs = algo_bytes / (kernel_ms * 1e-3) / 1e9
     if intensity >= RIDGE:
-        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+        roofline = {"bound": "mfma", "achieved": round(kernel_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4)}
     else:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
@@ -316,11 +362,13 @@ def main() -> int:
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kernel_ms, 5),
         "roofline": roofline,
+        **({"rotation": rotation} if rotation else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if not args.no_cpu:
         xb = x.view(torch.int16).numpy()
-        result["cpu_baseline"] = cpu_baseline(args.workload, xb, q.view(torch.uint8).numpy() if fp8 else q, s, b)
+        result["cpu_baseline"] = cpu_baseline(args.workload, xb, q.view(torch.uint8).numpy() if fp8 else q, s, b,
+                                              x32=x32)
     print(json.dumps(result), flush=True)
     return 0
 

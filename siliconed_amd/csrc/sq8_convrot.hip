@@ -13,8 +13,8 @@
 // Both are one pass over HBM. A 256-value chunk (a group of 256, or 256/G whole groups of a
 // smaller G) is four base-4 digits d0..d3 of the position p = d0 + 4·d1 + 16·d2 + 64·d3; the butterfly
 // stage of span 4^s runs over digit s. A thread holds 16 values whose positions differ in two
-// digits, so two stages run in its registers; one transposition through LDS brings the other two
-// digits into the registers, one more takes them back for contiguous stores.
+// digits, so the stages on those run in its registers; a transposition through LDS brings the
+// other two digits into the registers, one more takes them back.
 #include <hip/hip_runtime.h>
 
 #include "sq8_device.h"
@@ -50,7 +50,7 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-constexpr int PITCH = 272;  // floats per chunk in LDS: 256, padded so a wave's four chunks start 16 banks apart
+constexpr int PITCH = 272;  // floats per chunk in LDS: 256 + 4 per 64, so a wave's four chunks start 16 banks apart
 
 // Four consecutive values of a row, widened to fp32.
 template <bool X_BF16, bool VEC>
@@ -105,11 +105,14 @@ __device__ __forceinline__ void store4(void *y, int64_t at, const float *v) {
 // y = x·R per row, `stages` = log4(G). Each wave takes four 256-value chunks of the rows (chunk c of
 // row r: values [256c, 256c + 256), the last one of a row partial when k % 256 ≠ 0 — whole groups,
 // since k % G == 0; its missing values read as 0 and are never stored). Lane = 16·cc + l16: chunk
-// cc of the four, and in the loaded arrangement the values [16·l16, 16·l16 + 16) of it, register
-// r = d0 + 4·d1, l16 = d2 + 4·d3. Digits 0 and 1 are butterflied in registers; for 2 and 3 the
-// chunk goes through LDS to the arrangement l16 = d0 + 4·d1, r = d2 + 4·d3, and back. The LDS
-// copy of position p sits at 16·(p >> 4) + 4·(d1 ^ (p >> 6)) + d0 (16-byte slots swizzled), so
-// both the 16-byte writes and the 4-byte reads of the transposition meet 64 different banks.
+// cc of the four. Loaded arrangement: the lane holds positions 4·l16 + 64·u + e (register
+// r = e + 4u = d0 + 4·d3, l16 = d1 + 4·d2), so each load and store instruction covers 256
+// contiguous bytes of fp32 per chunk. Digit 0 is butterflied in registers; the chunk then goes
+// through LDS to the arrangement l16 = d0 + 4·d3, r = d1 + 4·d2 for digits 1 and 2, and back for
+// digit 3 — the stages in the reference's order. The LDS copy of position p sits at
+// p + 4·(p >> 6), so both the 16-byte writes and the 4-byte reads meet 64 different banks.
+// (The arrangement that keeps digits 0 and 1 in registers needs 64-byte-strided accesses per lane
+// and ran at 4.4 TB/s against this one's 5.9 on the C1 operand.)
 template <bool X_BF16, bool Y_BF16, bool VEC>
 __global__ void __launch_bounds__(256) rotate_groups_kernel(const void *x, int64_t ldx, void *y,
                                                             int64_t ldy, int64_t rows, int k, int stages, float norm,
@@ -122,53 +125,57 @@ __global__ void __launch_bounds__(256) rotate_groups_kernel(const void *x, int64
     for (int64_t qd = (int64_t)blockIdx.x * 4 + wave; qd < quads; qd += (int64_t)gridDim.x * 4) {
         const int64_t chunk = qd * 4 + cc;
         const int64_t row = chunk / cpr;
-        const int col0 = (int)(chunk - row * cpr) * 256 + 16 * l16;
+        const int base = (int)(chunk - row * cpr) * 256;
         const bool live = row < rows;
         float v[16];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            if (live && col0 + 4 * u < k) load4<X_BF16, VEC>(x, row * ldx + col0 + 4 * u, v + 4 * u);
+            const int col = base + 4 * l16 + 64 * u;
+            if (live && col < k) load4<X_BF16, VEC>(x, row * ldx + col, v + 4 * u);
             else v[4 * u] = v[4 * u + 1] = v[4 * u + 2] = v[4 * u + 3] = 0.0f;
         }
-        // Span 1 (digit 0), then span 4 (digit 1).
+        // Span 1 (digit 0).
 #pragma unroll
-        for (int d1 = 0; d1 < 4; ++d1) butterfly(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+        for (int u = 0; u < 4; ++u) butterfly(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]);
         if (stages > 1) {
 #pragma unroll
-            for (int d0 = 0; d0 < 4; ++d0) butterfly(v[d0], v[d0 + 4], v[d0 + 8], v[d0 + 12]);
-        }
-        if (stages > 2) {
-            const int sw = l16 >> 2;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<f32x4 *>(mine + 16 * l16 + 4 * (j ^ sw)) = f32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            for (int u = 0; u < 4; ++u)
+                *reinterpret_cast<f32x4 *>(mine + 4 * l16 + 68 * u) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
             wave_lds_sync();
-            // Now l16 = d0 + 4·d1 and register r = d2 + 4·d3: position l16 + 16·r.
+            // Now l16 = d0 + 4·d3 and register r = d1 + 4·d2: position d0 + 4·r + 64·d3.
+            const int d0 = l16 & 3, d3 = l16 >> 2;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) v[r] = mine[16 * r + 4 * ((l16 >> 2) ^ (r >> 2)) + (l16 & 3)];
-            // Span 16 (digit 2), then span 64 (digit 3).
+            for (int r = 0; r < 16; ++r) v[r] = mine[d0 + 4 * r + 68 * d3];
+            // Span 4 (digit 1), then span 16 (digit 2).
 #pragma unroll
-            for (int d3 = 0; d3 < 4; ++d3) butterfly(v[4 * d3], v[4 * d3 + 1], v[4 * d3 + 2], v[4 * d3 + 3]);
+            for (int d2 = 0; d2 < 4; ++d2) butterfly(v[4 * d2], v[4 * d2 + 1], v[4 * d2 + 2], v[4 * d2 + 3]);
+            if (stages > 2) {
+#pragma unroll
+                for (int d1 = 0; d1 < 4; ++d1) butterfly(v[d1], v[d1 + 4], v[d1 + 8], v[d1 + 12]);
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mine[d0 + 4 * r + 68 * d3] = v[r];
+            wave_lds_sync();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const f32x4 t = *reinterpret_cast<const f32x4 *>(mine + 4 * l16 + 68 * u);
+                v[4 * u] = t[0]; v[4 * u + 1] = t[1]; v[4 * u + 2] = t[2]; v[4 * u + 3] = t[3];
+            }
+            wave_lds_sync();
+            // Span 64 (digit 3).
             if (stages > 3) {
 #pragma unroll
-                for (int d2 = 0; d2 < 4; ++d2) butterfly(v[d2], v[d2 + 4], v[d2 + 8], v[d2 + 12]);
+                for (int e = 0; e < 4; ++e) butterfly(v[e], v[e + 4], v[e + 8], v[e + 12]);
             }
-            wave_lds_sync();
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mine[16 * r + 4 * ((l16 >> 2) ^ (r >> 2)) + (l16 & 3)] = v[r];
-            wave_lds_sync();
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 t = *reinterpret_cast<const f32x4 *>(mine + 16 * l16 + 4 * (j ^ sw));
-                v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
-            }
-            wave_lds_sync();
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = v[i] * norm;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (live && col0 + 4 * u < k) store4<Y_BF16, VEC>(y, row * ldy + col0 + 4 * u, v + 4 * u);
+        for (int u = 0; u < 4; ++u) {
+            const int col = base + 4 * l16 + 64 * u;
+            if (live && col < k) store4<Y_BF16, VEC>(y, row * ldy + col, v + 4 * u);
+        }
     }
 }
 
