@@ -200,6 +200,39 @@ int sq8_rotate_groups(sq8_ctx *ctx, const void *x, int x_dtype, int64_t ldx, voi
 int sq8_dequantize_rotated(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, int k, int n, int group,
                            const void *scale, int scale_dtype, int scale_layout, float *out, int64_t ldo);
 
+/* ---- W8A8: ComfyUI's int8_linear, the activation quantized per row (after its convrot rotation,
+ * if any), int8 × int8 products summed exactly in int32, C = act(float(Σ) · (s_x · s_w) + b)
+ * (Sources/Siliconed/TensorGEMMInt8.swift:4-37). Weights int8 only (w_dtype implied); k below 2^17
+ * (the int32 sums exact). ---- */
+
+/* **The activation's quantization**: per row of x (SQ8_F32 or SQ8_BF16, `rows` × k, leading
+ * dimension ldx), rotated by groups of `group` first (0: none; else 4, 16, 64 or 256 dividing k),
+ * s = max(max|y| / 127, 1e-30), codes = clamp(rint(y / s), −128, 127) — correctly rounded divisions,
+ * rint half to even; codes int8 [rows, ldq], scales fp32 [rows]. k up to 32 768 (else
+ * SQ8_EUNSUPPORTED). Replaces: `quantize_rows` / `quantize_held` (TensorGEMMInt8.swift:78-131),
+ * whose CPU statement is W8A8.quantize (:198-221). */
+int sq8_quantize_rows(sq8_ctx *ctx, const void *x, int x_dtype, int64_t ldx, int rows, int k, int group,
+                      int8_t *codes, int64_t ldq, float *scales);
+
+/* **The W8A8 product on a quantized activation**: codes int8 [m, ldq] with their row scales `sx`
+ * (fp32 [m]) — as sq8_quantize_rows writes them —, the int8 weight in `w_layout` (SQ8_PACKED(_GLU)
+ * as sq8_pack_weight stages it, SQ8_NK or SQ8_KN), `scale` fp32 per column or per tensor, `bias` fp32
+ * [n] or NULL, the epilogue fused; C fp32 or bf16 [m, n_out]. Replaces: submitQuantized with
+ * `prequantized` (TensorGEMMInt8.swift:237-281: the codes written by the operand's producer or the
+ * product before) — `linear_i8i8` then `scale_products`, with the bias and activation passes fused. */
+int sq8_linear_w8a8(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx,
+                    const void *w, int w_layout, int64_t ldw,
+                    const float *scale, int scale_layout, const float *bias, int epilogue,
+                    void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds);
+
+/* **The W8A8 route whole**: `a` (SQ8_F32 or SQ8_BF16) quantized per row (rotated by `group` first,
+ * 0 for none) into the context's scratch, then the product as sq8_linear_w8a8. Replaces:
+ * submitQuantized (TensorGEMMInt8.swift:237-281): quantize_rows → linear_i8i8 → scale_products. */
+int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group,
+                         const void *w, int w_layout, int64_t ldw,
+                         const float *scale, int scale_layout, const float *bias, int epilogue,
+                         void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds);
+
 /* ---- the elementwise passes of a DiT block around the products (all device pointers, queued) ---- */
 
 /* **Modulated RMSNorm to the next product's operand**: for each of `rows` rows of fp32 x (leading

@@ -60,6 +60,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "orc_rotation_norm": (ctypes.c_float, [I]),
         "orc_rotate_groups": (None, [P, I64, P, I64, I, I, I]),
         "orc_dequantize_rotated": (None, [P, I64, I, I, I, P, I, I, P, I64]),
+        "orc_quantize_rows": (None, [P, I64, I, I, I, P, I64, P]),
+        "orc_w8a8_product": (None, [P, I64, P, P, I, I64, P, I, I, I, I, P, I64]),
         "orc_gelu_tanh": (D, [D]),
         "orc_silu_glu": (D, [D, D]),
         "orc_situ": (D, [D, D]),
@@ -196,6 +198,32 @@ def dequantize_rotated(q: np.ndarray, group: int, scale: np.ndarray, scale_type:
     sc = np.ascontiguousarray(scale)
     lib().orc_dequantize_rotated(_p(q), n, k, n, group, _p(sc), scale_type, layout, _p(out), n)
     return out
+
+
+# ---- W8A8: Sources/Siliconed/TensorGEMMInt8.swift:4-37, 198-221 ------------------------------
+
+def quantize_rows(x: np.ndarray, group: int = 0):
+    """W8A8.quantize per row (TensorGEMMInt8.swift:198-221): int8 codes [rows, k], fp32 scales [rows]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    codes = np.empty((rows, k), dtype=np.int8)
+    scales = np.empty(rows, dtype=np.float32)
+    lib().orc_quantize_rows(_p(x), k, rows, k, int(group), _p(codes), k, _p(scales))
+    return codes, scales
+
+
+def w8a8_product(codes: np.ndarray, sx: np.ndarray, w: np.ndarray, w_kn: bool, sw: np.ndarray) -> np.ndarray:
+    """float(Σ codes·w) · (s_x · s_w), the sums exact: fp32 [m, n]."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    m, k = codes.shape
+    n = w.shape[1] if w_kn else w.shape[0]
+    sx = np.ascontiguousarray(sx, dtype=np.float32)
+    sw = np.ascontiguousarray(sw, dtype=np.float32)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_w8a8_product(_p(codes), k, _p(sx), _p(w), int(w_kn), w.shape[1], _p(sw), int(sw.size != 1), m, k, n,
+                           _p(c), n)
+    return c
 
 
 # ---- truth and judgement ------------------------------------------------------------------

@@ -271,6 +271,53 @@ void orc_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int grou
 }
 
 /* ---------------------------------------------------------------------------------------------
+ * W8A8: ComfyUI's int8_linear on a per-row quantized activation,
+ * Sources/Siliconed/TensorGEMMInt8.swift:4-37 (the recipe), :198-221 (W8A8.quantize).
+ * ------------------------------------------------------------------------------------------- */
+void orc_quantize_rows(const float *x, int64_t ldx, int rows, int k, int group, int8_t *codes, int64_t ldq,
+                       float *scales) {
+    /* Per row: y = x rotated by groups of `group` (none when 0: TensorGEMMInt8.swift:200-216, the
+     * butterflies of rotate_groups then × 1/√G), s = max(max|y| / 127, 1e-30) (an IEEE division),
+     * q = clamp(rint(y / s), −128, 127) (IEEE division, rint half to even). */
+#pragma omp parallel for schedule(static) if ((int64_t)rows * k > (1L << 18))
+    for (int r = 0; r < rows; ++r) {
+        float *y = (float *)malloc((size_t)(k > 0 ? k : 1) * sizeof(float));
+        if (group > 0) orc_rotate_groups(x + (int64_t)r * ldx, ldx, y, k, 1, k, group);
+        else memcpy(y, x + (int64_t)r * ldx, (size_t)k * sizeof(float));
+        float top = 0.0f;
+        for (int i = 0; i < k; ++i) top = fmaxf(top, fabsf(y[i]));
+        const float q = top / 127.0f;
+        const float scale = q > 1e-30f ? q : 1e-30f;
+        for (int i = 0; i < k; ++i) {
+            float c = rintf(y[i] / scale);
+            c = c < -128.0f ? -128.0f : (c > 127.0f ? 127.0f : c);
+            codes[(int64_t)r * ldq + i] = (int8_t)c;
+        }
+        scales[r] = scale;
+        free(y);
+    }
+}
+
+void orc_w8a8_product(const int8_t *codes, int64_t ldq, const float *sx, const int8_t *w, int w_kn, int64_t ldw,
+                      const float *sw, int sw_per_column, int m, int k, int n, float *c, int64_t ldc) {
+    /* acc = Σ codes·w exactly (int64 here; int32 in the kernel, exact for k < 2^17), then
+     * C = float(acc) · (s_x[row] · s_w[col]): the scale product first (TensorGEMMInt8.swift:19-31,
+     * `scale_products` :133-140). */
+#pragma omp parallel for schedule(static) if ((int64_t)m * n > 4096)
+    for (int r = 0; r < m; ++r) {
+        for (int j = 0; j < n; ++j) {
+            int64_t acc = 0;
+            for (int i = 0; i < k; ++i) {
+                const int8_t wv = w_kn ? w[(int64_t)i * ldw + j] : w[(int64_t)j * ldw + i];
+                acc += (int64_t)codes[(int64_t)r * ldq + i] * wv;
+            }
+            const float f = sx[r] * sw[sw_per_column ? j : 0];
+            c[(int64_t)r * ldc + j] = (float)(int32_t)acc * f;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------
  * Epilogues in double.
  * ------------------------------------------------------------------------------------------- */
 double orc_gelu_tanh(double x) {

@@ -69,6 +69,16 @@ void orc_rotate_groups(const float *x, int64_t ldx, float *y, int64_t ldy, int r
 void orc_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int group, const void *scale,
                             int scale_type, int layout, float *out, int64_t ldo);
 
+/* ---- W8A8 (ComfyUI's int8_linear): Sources/Siliconed/TensorGEMMInt8.swift:4-37, 198-221 ---- */
+/* Per row of x fp32 [rows, k]: rotated by groups of `group` (0: none) as orc_rotate_groups, then
+ * s = max(max|y| / 127, 1e-30), q = clamp(rint(y / s), −128, 127); codes int8 [rows, ldq], scales [rows]. */
+void orc_quantize_rows(const float *x, int64_t ldx, int rows, int k, int group, int8_t *codes, int64_t ldq,
+                       float *scales);
+/* C [m, n] = float(Σ codes·w) · (sx[row] · sw[col]), the sums exact; w int8 [k, n] (w_kn) or [n, k];
+ * sw per column or one (sw_per_column 0). */
+void orc_w8a8_product(const int8_t *codes, int64_t ldq, const float *sx, const int8_t *w, int w_kn, int64_t ldw,
+                      const float *sw, int sw_per_column, int m, int k, int n, float *c, int64_t ldc);
+
 /* ---- epilogues, in double (the definitions the GPU is judged against) ---- */
 /* nn.GELU(approximate="tanh") in double: Sources/Siliconed/QwenImage21.swift:953-963. */
 double orc_gelu_tanh(double x);

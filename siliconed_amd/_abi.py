@@ -33,6 +33,11 @@ SIGNATURES = {
                                 ctypes.POINTER(_D)]),
     "sq8_rotate_groups": (_I, [_P, _P, _I, _I64, _P, _I, _I64, _I, _I, _I]),
     "sq8_dequantize_rotated": (_I, [_P, _P, _I64, _I, _I, _I, _P, _I, _I, _P, _I64]),
+    "sq8_quantize_rows": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P, _I64, _P]),
+    "sq8_linear_w8a8": (_I, [_P, _P, _I64, _P, _P, _I, _I64, _P, _I, _P, _I, _P, _I, _I64, _I, _I, _I,
+                             ctypes.POINTER(_D)]),
+    "sq8_linear_quantized": (_I, [_P, _P, _I, _I64, _I, _P, _I, _I64, _P, _I, _P, _I, _P, _I, _I64, _I, _I, _I,
+                                  ctypes.POINTER(_D)]),
     "sq8_packed_bytes": (_I64, [_I, _I, _I]),
     "sq8_pack_weight": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P]),
     "sq8_dequantize": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _I, _I64, _I64, _P]),

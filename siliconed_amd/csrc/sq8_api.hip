@@ -8,6 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 
 #include "sq8_gemm.h"
@@ -114,6 +115,11 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
     if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
+    // The kernels address A and W with 32-bit byte offsets from their bases.
+    if ((int64_t)q.m * (q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
+        (is_packed(q.w_layout) ? sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue))
+                               : (int64_t)(q.w_layout == SQ8_KN ? q.k : q.n) * q.ldw) > (int64_t)UINT32_MAX)
+        return SQ8_EUNSUPPORTED;
 
     DeviceScope scope(ctx->device);
     if (scope.error != hipSuccess) return hip_status(scope.error);
@@ -236,6 +242,121 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
                           (q.w_layout == SQ8_NK || (cols_per_half % 4) == 0);
         e = sq8::launch_gemm(p, fast, tile, wt, wl, q.epilogue, out, ctx->stream);
     }
+    if (e != hipSuccess) return hip_status(e);
+    if (gpu_seconds) {
+        e = hipEventRecord(ctx->end, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->end);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->begin, ctx->end);
+        if (e != hipSuccess) return hip_status(e);
+        *gpu_seconds = (double)ms * 1e-3;
+    }
+    return SQ8_OK;
+}
+
+// The W8A8 product: codes [m, ldq] int8 with row scales sx (already quantized, or quantized here
+// from `a` when `a` is non-null), the int8 weight packed or [N, K] (repacked into the context's
+// buffer otherwise), C = act(float(Σ) · (s_x · s_w) + b).
+struct W8A8 {
+    const void *a; int a_dtype; int64_t lda; int group;     // quantized here when a != nullptr
+    const int8_t *codes; int64_t ldq; const float *sx;       // else these
+    const void *w; int w_layout; int64_t ldw;
+    const float *scale; int scale_layout; const float *bias; int epilogue;
+    void *c; int c_dtype; int64_t ldc;
+    int m, k, n;
+};
+
+int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
+    if (!ctx) return SQ8_EINVAL;
+    int st = check_config(SQ8_BF16, SQ8_INT8, q.w_layout, q.scale_layout, q.c_dtype, q.epilogue);
+    if (st != SQ8_OK) return st;
+    if (q.a && q.a_dtype != SQ8_F32 && q.a_dtype != SQ8_BF16) return SQ8_EUNSUPPORTED;
+    if (q.m < 0 || q.k < 0 || q.n < 0) return SQ8_EINVAL;
+    if (is_glu(q.epilogue) && (q.n % 2) != 0) return SQ8_EINVAL;
+    if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
+    if (q.k >= (1 << 17)) return SQ8_EUNSUPPORTED;  // the int32 sums stay exact below 2^17 terms
+    if (q.a && q.k > sq8::quantize_row_limit()) return SQ8_EUNSUPPORTED;
+    const int n_out = is_glu(q.epilogue) ? q.n / 2 : q.n;
+    if (gpu_seconds) *gpu_seconds = 0.0;
+    if (q.m == 0 || n_out == 0) return SQ8_OK;
+    if (q.k == 0) return SQ8_EUNSUPPORTED;
+    if (!q.w || !q.scale || !q.c) return SQ8_EINVAL;
+    if (q.a ? q.lda < q.k : (!q.codes || !q.sx || q.ldq < q.k)) return SQ8_EINVAL;
+    if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
+    if (q.ldc < n_out) return SQ8_EINVAL;
+    const int k_pad = (q.k + 127) / 128 * 128;
+    // The kernel addresses the codes and the weight with 32-bit byte offsets from their bases.
+    if ((int64_t)q.m * std::max<int64_t>(k_pad, q.ldq) > (int64_t)UINT32_MAX ||
+        std::max<int64_t>(sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue)),
+                          is_packed(q.w_layout) ? 0 : (int64_t)(q.w_layout == SQ8_KN ? q.k : q.n) * q.ldw) >
+            (int64_t)UINT32_MAX)
+        return SQ8_EUNSUPPORTED;
+
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    // Scratch: codes [m, k_pad] (when quantized or padded here), then the row scales.
+    const bool own_codes = q.a || q.k % 128 != 0 || q.ldq % 16 != 0 || !aligned(q.codes, 16);
+    const size_t code_bytes = own_codes ? ((size_t)q.m * (size_t)k_pad + 255) / 256 * 256 : 0;
+    const size_t bytes = code_bytes + (q.a ? (size_t)q.m * 4 : 0);
+    if (bytes > 0) {
+        st = reserve_scratch(ctx, bytes);
+        if (st != SQ8_OK) return st;
+    }
+    int8_t *codes = own_codes ? static_cast<int8_t *>(ctx->scratch) : const_cast<int8_t *>(q.codes);
+    const float *sx = q.a ? reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + code_bytes) : q.sx;
+    const int64_t ldq = own_codes ? k_pad : q.ldq;
+    if (gpu_seconds) {
+        hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    hipError_t e = hipSuccess;
+    if (q.a)
+        e = sq8::launch_quantize_rows(q.a, q.a_dtype == SQ8_BF16, q.lda, q.m, q.k, q.group, codes, ldq, k_pad,
+                                      const_cast<float *>(sx), ctx->stream);
+    else if (own_codes)
+        e = sq8::launch_pad_codes(q.codes, q.ldq, codes, ldq, q.m, q.k, k_pad, ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+
+    sq8::GemmArgs p;
+    memset(&p, 0, sizeof(p));
+    p.a = reinterpret_cast<const uint16_t *>(codes);
+    p.lda = ldq;
+    p.sx = sx;
+    p.scale = q.scale;
+    p.bias = q.bias;
+    p.c[0] = q.c;
+    p.ldc = q.ldc;
+    p.M = q.m;
+    p.N = q.n;
+    p.K = q.k;
+    p.glu_half = is_glu(q.epilogue) ? q.n / 2 : 0;
+    p.scale_per_col = q.scale_layout == SQ8_SCALE_COLUMNS;
+    const size_t esz = q.c_dtype == SQ8_F32 ? 4 : 2;
+    p.c_vec = aligned(q.c, 4 * esz) && (q.ldc % 4) == 0;
+    p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
+    p.sb_vec = aligned(q.scale, 16) && (!q.bias || aligned(q.bias, 16)) && (p.glu_half % 4) == 0;
+    p.kt = k_pad / 128;
+    // The weight: packed as staged, [N, K] read in place when its rows hold whole steps, else
+    // repacked per product into the context's buffer.
+    int wl = sq8::W_PACKED;
+    p.w = static_cast<const uint8_t *>(q.w);
+    if (is_packed(q.w_layout)) {
+        p.kt_w = (q.k + 63) / 64;
+    } else if (q.w_layout == SQ8_NK && !is_glu(q.epilogue) && q.k % 128 == 0 && q.ldw % 16 == 0 && aligned(q.w, 16)) {
+        wl = sq8::W_NK;
+        p.ldw = q.ldw;
+        p.kt_w = q.k / 64;
+    } else {
+        const int64_t wbytes = sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue));
+        st = reserve_buffer(ctx, &ctx->wpack, &ctx->wpack_bytes, (size_t)wbytes);
+        if (st != SQ8_OK) return st;
+        e = sq8::launch_pack(static_cast<const uint8_t *>(q.w), q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK, q.ldw, q.k,
+                             q.n, is_glu(q.epilogue), static_cast<uint8_t *>(ctx->wpack), ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        p.w = static_cast<const uint8_t *>(ctx->wpack);
+        p.kt_w = (q.k + 63) / 64;
+    }
+    e = sq8::launch_i8gemm(p, wl, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16, ctx->stream);
     if (e != hipSuccess) return hip_status(e);
     if (gpu_seconds) {
         e = hipEventRecord(ctx->end, ctx->stream);
@@ -391,6 +512,48 @@ int sq8_dequantize_rotated(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, int k
     if (scope.error != hipSuccess) return hip_status(scope.error);
     return hip_status(sq8::launch_dequantize_rotated(codes, ldq, k, n, group, scale, scale_dtype,
                                                      scale_layout == SQ8_SCALE_COLUMNS, out, ldo, ctx->stream));
+}
+
+int sq8_quantize_rows(sq8_ctx *ctx, const void *x, int x_dtype, int64_t ldx, int rows, int k, int group, int8_t *codes,
+                      int64_t ldq, float *scales) {
+    if (!ctx || rows < 0 || k < 0) return SQ8_EINVAL;
+    if (x_dtype != SQ8_F32 && x_dtype != SQ8_BF16) return SQ8_EUNSUPPORTED;
+    if (group != 0 && (!sq8::is_rotation_group(group) || k % group != 0)) return SQ8_EINVAL;
+    if (k > sq8::quantize_row_limit()) return SQ8_EUNSUPPORTED;
+    if (rows == 0) return SQ8_OK;
+    if (!x || !codes || !scales || ldx < k || ldq < k) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_quantize_rows(x, x_dtype == SQ8_BF16, ldx, rows, k, group, codes, ldq, k, scales,
+                                                ctx->stream));
+}
+
+int sq8_linear_w8a8(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx, const void *w, int w_layout,
+                    int64_t ldw, const float *scale, int scale_layout, const float *bias, int epilogue, void *c,
+                    int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    W8A8 q;
+    memset(&q, 0, sizeof(q));
+    q.codes = codes; q.ldq = ldq; q.sx = sx;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    return run_w8a8(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group, const void *w, int w_layout,
+                         int64_t ldw, const float *scale, int scale_layout, const float *bias, int epilogue, void *c,
+                         int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    if (!a && m > 0) return SQ8_EINVAL;
+    W8A8 q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda; q.group = group;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    if (!a) return m == 0 ? SQ8_OK : SQ8_EINVAL;
+    return run_w8a8(ctx, q, gpu_seconds);
 }
 
 int64_t sq8_packed_bytes(int k, int n, int glu) {

@@ -19,66 +19,14 @@
 
 #include "sq8_device.h"
 #include "sq8_gemm.h"
+#include "sq8_rotate.h"
 
 namespace sq8 {
 namespace {
 
-// The 4-point butterfly of rotate_groups: p = a + b, m = a − b, u = c + d, w = c − d, then
-// (p + w, p − w, m + u, u − m) — each sum rounded to fp32 on its own (no contraction here).
-__device__ __forceinline__ void butterfly(float &a, float &b, float &c, float &d) {
-    const float p = a + b, m = a - b, u = c + d, w = c - d;
-    a = p + w;
-    b = p - w;
-    c = m + u;
-    d = u - m;
-}
-
-// The same on integers (exact).
-__device__ __forceinline__ void butterfly(int &a, int &b, int &c, int &d) {
-    const int p = a + b, m = a - b, u = c + d, w = c - d;
-    a = p + w;
-    b = p - w;
-    c = m + u;
-    d = u - m;
-}
-
-// Orders one wave's LDS writes before its later reads of other lanes' values. The LDS runs a
-// wave's operations in issue order; these fences only keep the compiler from reordering them.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-constexpr int PITCH = 272;  // floats per chunk in LDS: 256 + 4 per 64, so a wave's four chunks start 16 banks apart
-
-// Four consecutive values of a row, widened to fp32.
-template <bool X_BF16, bool VEC>
-__device__ __forceinline__ void load4(const void *x, int64_t at, float *v) {
-    if constexpr (X_BF16) {
-        const uint16_t *p = static_cast<const uint16_t *>(x) + at;
-        if constexpr (VEC) {
-            const u32x2 d = *reinterpret_cast<const u32x2 *>(p);
-            v[0] = __uint_as_float(d[0] << 16);
-            v[1] = __uint_as_float(d[0] & 0xFFFF0000u);
-            v[2] = __uint_as_float(d[1] << 16);
-            v[3] = __uint_as_float(d[1] & 0xFFFF0000u);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = __uint_as_float((uint32_t)p[e] << 16);
-        }
-    } else {
-        const float *p = static_cast<const float *>(x) + at;
-        if constexpr (VEC) {
-            const f32x4 d = *reinterpret_cast<const f32x4 *>(p);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = d[e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = p[e];
-        }
-    }
-}
+using rot::butterfly;
+using rot::load4;
+using rot::PITCH;
 
 template <bool Y_BF16, bool VEC>
 __device__ __forceinline__ void store4(void *y, int64_t at, const float *v) {
@@ -104,15 +52,10 @@ __device__ __forceinline__ void store4(void *y, int64_t at, const float *v) {
 
 // y = x·R per row, `stages` = log4(G). Each wave takes four 256-value chunks of the rows (chunk c of
 // row r: values [256c, 256c + 256), the last one of a row partial when k % 256 ≠ 0 — whole groups,
-// since k % G == 0; its missing values read as 0 and are never stored). Lane = 16·cc + l16: chunk
-// cc of the four. Loaded arrangement: the lane holds positions 4·l16 + 64·u + e (register
-// r = e + 4u = d0 + 4·d3, l16 = d1 + 4·d2), so each load and store instruction covers 256
-// contiguous bytes of fp32 per chunk. Digit 0 is butterflied in registers; the chunk then goes
-// through LDS to the arrangement l16 = d0 + 4·d3, r = d1 + 4·d2 for digits 1 and 2, and back for
-// digit 3 — the stages in the reference's order. The LDS copy of position p sits at
-// p + 4·(p >> 6), so both the 16-byte writes and the 4-byte reads meet 64 different banks.
-// (The arrangement that keeps digits 0 and 1 in registers needs 64-byte-strided accesses per lane
-// and ran at 4.4 TB/s against this one's 5.9 on the C1 operand.)
+// since k % G == 0; its missing values read as 0 and are never stored), one per group of 16 lanes,
+// held and rotated as rot::rotate_chunk describes. (An arrangement that keeps digits 0 and 1 in
+// registers needs 64-byte-strided accesses per lane and ran at 4.4 TB/s against this one's 5.9 on
+// the C1 operand.)
 template <bool X_BF16, bool Y_BF16, bool VEC>
 __global__ void __launch_bounds__(256) rotate_groups_kernel(const void *x, int64_t ldx, void *y,
                                                             int64_t ldy, int64_t rows, int k, int stages, float norm,
@@ -134,41 +77,7 @@ __global__ void __launch_bounds__(256) rotate_groups_kernel(const void *x, int64
             if (live && col < k) load4<X_BF16, VEC>(x, row * ldx + col, v + 4 * u);
             else v[4 * u] = v[4 * u + 1] = v[4 * u + 2] = v[4 * u + 3] = 0.0f;
         }
-        // Span 1 (digit 0).
-#pragma unroll
-        for (int u = 0; u < 4; ++u) butterfly(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]);
-        if (stages > 1) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                *reinterpret_cast<f32x4 *>(mine + 4 * l16 + 68 * u) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
-            wave_lds_sync();
-            // Now l16 = d0 + 4·d3 and register r = d1 + 4·d2: position d0 + 4·r + 64·d3.
-            const int d0 = l16 & 3, d3 = l16 >> 2;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) v[r] = mine[d0 + 4 * r + 68 * d3];
-            // Span 4 (digit 1), then span 16 (digit 2).
-#pragma unroll
-            for (int d2 = 0; d2 < 4; ++d2) butterfly(v[4 * d2], v[4 * d2 + 1], v[4 * d2 + 2], v[4 * d2 + 3]);
-            if (stages > 2) {
-#pragma unroll
-                for (int d1 = 0; d1 < 4; ++d1) butterfly(v[d1], v[d1 + 4], v[d1 + 8], v[d1 + 12]);
-            }
-            wave_lds_sync();
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mine[d0 + 4 * r + 68 * d3] = v[r];
-            wave_lds_sync();
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const f32x4 t = *reinterpret_cast<const f32x4 *>(mine + 4 * l16 + 68 * u);
-                v[4 * u] = t[0]; v[4 * u + 1] = t[1]; v[4 * u + 2] = t[2]; v[4 * u + 3] = t[3];
-            }
-            wave_lds_sync();
-            // Span 64 (digit 3).
-            if (stages > 3) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) butterfly(v[e], v[e + 4], v[e + 8], v[e + 12]);
-            }
-        }
+        rot::rotate_chunk(v, mine, l16, stages);
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = v[i] * norm;
 #pragma unroll
@@ -266,12 +175,6 @@ __global__ void __launch_bounds__(256) dequantize_rotated_kernel(const int8_t *_
     }
 }
 
-int stages_of(int group) {
-    int s = 0;
-    for (int g = 1; g < group; g *= 4) ++s;
-    return s;
-}
-
 }  // namespace
 
 bool is_rotation_group(int group) { return group == 4 || group == 16 || group == 64 || group == 256; }
@@ -283,7 +186,7 @@ hipError_t launch_rotate_groups(const void *x, bool x_bf16, int64_t ldx, void *y
     const int64_t quads = (chunks + 3) / 4;
     const int64_t want = (quads + 3) / 4;
     const dim3 grid((unsigned)(want < 16384 ? want : 16384));
-    const int stages = stages_of(group);
+    const int stages = rot::stages_of(group);
     const float norm = 1.0f / sqrtf((float)group);
     const size_t xa = x_bf16 ? 8 : 16, ya = y_bf16 ? 8 : 16;
     const bool vec = (reinterpret_cast<uintptr_t>(x) % xa) == 0 && (reinterpret_cast<uintptr_t>(y) % ya) == 0 &&
@@ -311,7 +214,7 @@ hipError_t launch_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n,
     if (k == 0 || n == 0) return hipSuccess;
     const int tiles_n = (n + 63) / 64, tiles_k = (k + 255) / 256;
     const dim3 grid((unsigned)((int64_t)tiles_n * tiles_k));
-    const int stages = stages_of(group);
+    const int stages = rot::stages_of(group);
     const float norm = 1.0f / sqrtf((float)group);
     const bool vec = n % 4 == 0 && ldq % 4 == 0 && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(q) % 4) == 0 &&
                      (reinterpret_cast<uintptr_t>(out) % 16) == 0;

@@ -27,8 +27,10 @@ struct GemmArgs {
     int a_vec, w_vec, c_vec; // 16-byte loads of A, wide loads of W, wide stores of C allowed
     int c_vec16;            // 16-byte stores of C allowed (aligned base, stride, split and head size)
     int sb_vec;             // 16-byte loads of 4 scales / biases allowed (aligned bases, GLU half % 4 == 0)
-    int kt;                 // K steps of 64 (the packed layout's K extent)
+    int kt;                 // K steps of 64 (the packed layout's K extent); W8A8: K steps of 128
     int tiles_m, tiles_n;   // set by the launcher
+    const float *sx;        // W8A8: the activation's row scales fp32 [M] (`a` then holds int8 codes)
+    int kt_w;               // W8A8: K steps of 64 of the packed weight
 };
 
 enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };
@@ -73,6 +75,18 @@ hipError_t launch_rotate_groups(const void *x, bool x_bf16, int64_t ldx, void *y
                                 int k, int group, hipStream_t stream);
 hipError_t launch_dequantize_rotated(const int8_t *q, int64_t ldq, int k, int n, int group, const void *scale,
                                      int scale_dtype, bool per_column, float *out, int64_t ldo, hipStream_t stream);
+
+// W8A8 (sq8_w8a8.hip, sq8_i8_inst.hip): the activation's per-row quantization (optionally rotated
+// first) into int8 codes of rows k_pad ≥ k bytes (zero past k) and fp32 row scales; rows up to
+// quantize_row_limit() values. The int8 × int8 product: `a` the codes (lda a multiple of 16,
+// 16-byte aligned, kt = k_pad / 128 steps, zero past K), `sx` their scales, the weight packed
+// (kt_w = its 64-steps) or [N, K] with K a multiple of 128.
+int quantize_row_limit();
+hipError_t launch_quantize_rows(const void *x, bool x_bf16, int64_t ldx, int rows, int k, int group, int8_t *codes,
+                                int64_t ldq, int k_pad, float *scales, hipStream_t stream);
+hipError_t launch_pad_codes(const int8_t *src, int64_t ld_src, int8_t *dst, int64_t ld_dst, int64_t rows, int k, int k_pad,
+                            hipStream_t stream);
+hipError_t launch_i8gemm(const GemmArgs &p, int wl, int epi, int out, hipStream_t stream);
 
 // The DiT block's elementwise passes (sq8_block.hip).
 hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,

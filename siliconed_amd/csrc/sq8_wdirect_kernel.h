@@ -74,12 +74,15 @@ __device__ __forceinline__ bf16x8 widen8(uint32_t d0, uint32_t d1) {
 }
 
 // Byte offset (K step 0) of the 16 bytes lane `lane`, load j (block j>>1, half j&1) reads for
-// virtual 64-column slab `slab`. Past the edge of an [N, K] weight: the last column of the same half
-// (its results are never stored).
+// virtual 64-column slab `slab`. Past the edge of an [N, K] weight: the last column of the same half;
+// past the last slab of a packed weight (a tile's waves outnumber the slabs left): the last slab —
+// results never stored, reads kept inside the buffer.
 template <int WL, bool GLU>
 __device__ __forceinline__ uint32_t w_offset(const GemmArgs &p, int slab, int j, int lane) {
     if constexpr (WL == W_PACKED) {
-        return (uint32_t)(((int64_t)slab * p.kt * 4 + j) * 1024 + lane * 16);
+        const int slabs = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
+        const int s = slab < slabs ? slab : slabs - 1;
+        return (uint32_t)(((int64_t)s * p.kt * 4 + j) * 1024 + lane * 16);
     } else {
         const int b = j >> 1, c = j & 1, h = lane >> 5, nl = lane & 31;
         int n;

@@ -133,7 +133,7 @@ class TensorGEMM:
     def linear(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
                c: torch.Tensor, m: int, k: int, n: int, weight_offset: int = 0, scales_offset: int = 0,
                block: Optional[int] = None, rotation=None, rounding: bool = True, quantizing=None,
-               settled: bool = False, layout: str = "kn", bias: Optional[torch.Tensor] = None,
+               prequantized=None, settled: bool = False, layout: str = "kn", bias: Optional[torch.Tensor] = None,
                epilogue=None, fp8: Optional[bool] = None) -> float:
         """`linear(a:int8:weightOffset:scales:scalesOffset:perColumn:…:c:m:k:n:settled:)`
         (TensorGEMM.swift:264-290): C[m, n] = A[m, k] · (q · s), q `[k, n]` (`layout="kn"`, the
@@ -145,15 +145,23 @@ class TensorGEMM:
         own), the activation rotated by it first (TensorGEMMBF16.swift:222-233). Returns the GPU
         seconds, 0 when `settled` (queued).
 
+        `quantizing` (truthy, or the reference's `(buffer, codesOffset, scalesOffset, rows)`, whose
+        reserve this library replaces with its own scratch): the W8A8 route — `a` quantized per row
+        (after the rotation) and the int8 × int8 product (submitQuantized, TensorGEMMInt8.swift:237-281);
+        `prequantized` = (codes, scales) of `a` already quantized skips that pass.
+
         Routes this library does not take raise `abi.Unsupported` before any work, as the
         reference's `nil` pipelines send the caller back to the widened route: Q8_0 `block`
-        scales, W8A8 `quantizing`, an fp32 activation not rounded.
+        scales, an fp32 activation not rounded.
         """
         if block is not None:
             raise abi.Unsupported(abi.EUNSUPPORTED, "Q8_0 block scales")
         group = 0 if rotation is None else int(rotation[0] if isinstance(rotation, (tuple, list)) else rotation)
-        if quantizing is not None:
-            raise abi.Unsupported(abi.EUNSUPPORTED, "W8A8 activation quantization")
+        if quantizing is not None or prequantized is not None:
+            if fp8:
+                raise abi.Unsupported(abi.EUNSUPPORTED, "W8A8 takes int8 weights")
+            return self._w8a8_linear(a, int8, scales, per_column, c, m, k, n, weight_offset, scales_offset, group,
+                                     prequantized, settled, layout, bias, epilogue)
         if a.dtype == torch.float32 and not rounding:
             raise abi.Unsupported(abi.EUNSUPPORTED, "fp32 activations without bf16 rounding")
         lay = _LAYOUTS[layout]
@@ -179,6 +187,102 @@ class TensorGEMM:
         name = "sq8_linear_rotated" if group else "sq8_linear"
         abi.check(getattr(abi.load(), name)(*args), name)
         return 0.0 if settled else secs.value
+
+    def _w8a8_linear(self, a, int8, scales, per_column, c, m, k, n, weight_offset, scales_offset, group, prequantized,
+                     settled, layout, bias, epilogue) -> float:
+        lay = _LAYOUTS[layout]
+        epi = _epilogue(epilogue)
+        n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
+        if c.numel() < m * n_out or int8.numel() < weight_offset + k * n:
+            raise ValueError("c or the weight buffer too small")
+        if scales.dtype != torch.float32 or scales.numel() * 4 < scales_offset + 4 * (n if per_column else 1):
+            raise ValueError("scales must be fp32, n of them (or one) after the offset")
+        ldw = n if lay == abi.KN else k
+        secs = ctypes.c_double(0.0)
+        common = (_dev(int8, "int8") + weight_offset, lay, ldw,
+                  _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
+                  None if bias is None else _dev(bias, "bias"), epi,
+                  _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n, None if settled else ctypes.byref(secs))
+        if prequantized is not None:
+            codes, sx = prequantized
+            st = abi.load().sq8_linear_w8a8(self._h, _dev(codes, "codes"), _row_major(codes, "codes"),
+                                            _dev(sx, "scales"), *common)
+            abi.check(st, "sq8_linear_w8a8")
+        else:
+            st = abi.load().sq8_linear_quantized(self._h, _dev(a, "a"), _adtype(a), k, group, *common)
+            abi.check(st, "sq8_linear_quantized")
+        return 0.0 if settled else secs.value
+
+    # ---- W8A8 (ComfyUI's int8_linear) ----------------------------------------------------------
+
+    def quantize_rows(self, x: torch.Tensor, group: int = 0, *, codes: Optional[torch.Tensor] = None,
+                      scales: Optional[torch.Tensor] = None):
+        """Per-row int8 quantization of x [rows, k] (fp32 or bf16), rotated by groups of `group`
+        first (0: none): (codes int8 [rows, k], scales fp32 [rows]) — W8A8.quantize's bits
+        (TensorGEMMInt8.swift:198-221)."""
+        if x.dim() != 2:
+            raise ValueError("x must be 2-D [rows, k]")
+        rows, k = x.shape
+        if codes is None:
+            codes = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+        if scales is None:
+            scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+        if codes.dtype != torch.int8 or tuple(codes.shape) != (rows, k) or scales.dtype != torch.float32:
+            raise ValueError("codes int8 [rows, k], scales fp32 [rows]")
+        st = abi.load().sq8_quantize_rows(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"), rows, k, int(group),
+                                          _dev(codes, "codes"), _row_major(codes, "codes"), _dev(scales, "scales"))
+        abi.check(st, "sq8_quantize_rows")
+        return codes, scales
+
+    def _w8a8_product(self, name, lead, m, k, w, scale, layout, bias, epilogue, out, out_dtype, timed, device):
+        epi = _epilogue(epilogue)
+        if isinstance(w, PackedWeight):
+            if w.w_dtype != abi.INT8:
+                raise ValueError("W8A8 takes int8 weights")
+            lay, n, ldw, wptr = w.layout, w.n, w.k, _dev(w.data, "w")
+            if w.k != k:
+                raise ValueError(f"the packed weight has K = {w.k}, the activation {k}")
+        else:
+            if w.dtype != torch.int8 or w.dim() != 2:
+                raise ValueError("W8A8 takes an int8 weight [n, k] (nk) or [k, n] (kn)")
+            lay = _LAYOUTS[layout]
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            ldw, wptr = _row_major(w, "w"), _dev(w, "w")
+        glu = epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU)
+        n_out = n // 2 if glu else n
+        per_col = scale.numel() != 1
+        if scale.dtype != torch.float32 or (per_col and scale.numel() != n):
+            raise ValueError("scale must be fp32 with n entries (or one)")
+        if out is None:
+            out = torch.empty((m, n_out), dtype=out_dtype, device=device)
+        secs = ctypes.c_double(0.0)
+        st = getattr(abi.load(), name)(self._h, *lead, wptr, lay, ldw, _dev(scale, "scale"),
+                                       abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
+                                       None if bias is None else _dev(bias, "bias"), epi, _dev(out, "out"),
+                                       _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+                                       ctypes.byref(secs) if timed else None)
+        abi.check(st, name)
+        return (out, secs.value) if timed else out
+
+    def product_w8a8(self, codes: torch.Tensor, sx: torch.Tensor, w, scale: torch.Tensor, *, layout: str = "nk",
+                     bias: Optional[torch.Tensor] = None, epilogue=None, out: Optional[torch.Tensor] = None,
+                     out_dtype: torch.dtype = torch.bfloat16, timed: bool = False):
+        """act(float(codes · qᵀ) · (s_x · s_w) + b) on an activation already quantized (codes int8
+        [m, k], sx fp32 [m]); W int8 [n, k] (`nk`), [k, n] (`kn`) or a PackedWeight."""
+        if codes.dtype != torch.int8 or sx.dtype != torch.float32:
+            raise ValueError("codes int8 [m, k], sx fp32 [m]")
+        m, k = codes.shape
+        return self._w8a8_product("sq8_linear_w8a8", (_dev(codes, "codes"), _row_major(codes, "codes"), _dev(sx, "sx")),
+                                  m, k, w, scale, layout, bias, epilogue, out, out_dtype, timed, codes.device)
+
+    def product_quantized(self, x: torch.Tensor, w, scale: torch.Tensor, *, group: int = 0, layout: str = "nk",
+                          bias: Optional[torch.Tensor] = None, epilogue=None, out: Optional[torch.Tensor] = None,
+                          out_dtype: torch.dtype = torch.bfloat16, timed: bool = False):
+        """The W8A8 route whole: x (fp32 or bf16 [m, k]) quantized per row (rotated by `group`
+        first), then the int8 × int8 product as `product_w8a8`."""
+        m, k = x.shape
+        return self._w8a8_product("sq8_linear_quantized", (_dev(x, "x"), _adtype(x), _row_major(x, "x"), int(group)),
+                                  m, k, w, scale, layout, bias, epilogue, out, out_dtype, timed, x.device)
 
     # ---- staging -----------------------------------------------------------------------------
 

@@ -381,3 +381,86 @@ def test_rotate_groups_is_its_own_inverse_within_rounding(orc):
         stages = 2 * int(round(math.log(g, 4)))
         assert np.abs(back - x).max() <= 4 * stages * 2.0 ** -24 * np.abs(x).max() * math.sqrt(g) / 4 + 1e-6
         assert np.abs(back - x).max() > 0 or g == 4
+
+
+# ---- W8A8: Sources/Siliconed/TensorGEMMInt8.swift:4-37, 198-221 ------------------------------------
+
+def test_quantize_rows_rounds_half_to_even(orc):
+    # max|y| = 127 → scale exactly 1: the codes are rint of the values themselves, half to even
+    # (torch.round, not half away from zero: 2.5 → 2, −0.5 → 0, 63.5 → 64).
+    x = np.array([[127.0, 63.5, -0.5, 1.5, 2.5, 0.0, -126.5, 3.49]], np.float32)
+    codes, scales = orc.quantize_rows(x)
+    assert scales[0] == 1.0
+    assert codes[0].tolist() == [127, 64, 0, 2, 2, 0, -126, 3]
+
+
+def test_quantize_rows_divides_correctly(orc):
+    # Found by search and checked with numpy's IEEE division: s = m/127 correctly rounded, and
+    # y/s correctly rounded before rint — a reciprocal's product (y·(1/s)) gives 97 here, the
+    # division 96; and m·(1/127) is not m/127 for m = 0.6864249110221863.
+    m, y = np.float32(2.166764259338379), np.float32(1.646399736404419)
+    codes, scales = orc.quantize_rows(np.array([[m, y, -y]], np.float32))
+    s = np.float32(m / np.float32(127))
+    assert scales[0] == s and codes[0].tolist() == [127, 96, -96]
+    assert np.rint(np.float32(y * np.float32(np.float32(1) / s))) == 97
+    m2 = np.float32(0.6864249110221863)
+    _, s2 = orc.quantize_rows(np.array([[m2]], np.float32))
+    assert s2[0] == np.float32(m2 / np.float32(127)) != np.float32(m2 * (np.float32(1) / np.float32(127)))
+
+
+def test_quantize_rows_floor_and_extremes(orc):
+    # A row of zeros takes the floor scale 1e-30 (codes 0); the largest value maps to ±127 exactly
+    # and no code leaves [−127, 127] although the clamp allows −128.
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((6, 520)) * 4).astype(np.float32)
+    x[2] = 0
+    x[4, 17] = -300.0
+    codes, scales = orc.quantize_rows(x)
+    assert scales[2] == np.float32(1e-30) and not codes[2].any()
+    assert codes[4, 17] == -127 and codes.min() >= -127 and codes.max() <= 127
+    for r in range(6):
+        if r != 2:
+            assert np.abs(codes[r]).max() == 127
+
+
+@pytest.mark.parametrize("g", [0, 16, 64, 256])
+def test_quantize_rows_against_numpy(orc, g):
+    # The recipe in numpy's own IEEE fp32 operations on the oracle's rotated row (the rotation is
+    # pinned above): max, the divide by 127, the 1e-30 floor, the divide, rint, the clamp.
+    rng = np.random.default_rng(g + 1)
+    x = (rng.standard_normal((9, 768)) * 3).astype(np.float32)
+    x[:, 300] *= 300
+    y = orc.rotate_groups(x, g) if g else x
+    s = np.maximum(np.abs(y).max(axis=1) / np.float32(127), np.float32(1e-30)).astype(np.float32)
+    q = np.clip(np.rint(y / s[:, None]), -128, 127).astype(np.int8)
+    codes, scales = orc.quantize_rows(x, g)
+    assert np.array_equal(scales, s) and np.array_equal(codes, q)
+
+
+def test_w8a8_product_is_exact_then_scaled(orc):
+    # int64 numpy products (exact); the fp32 conversion of a sum past 2^24 rounds half to even;
+    # the scale product s_x·s_w is formed first: with acc = −284410, s_x = 0.05983570218086243,
+    # s_w = 0.007420313078910112 (found by search), (acc·s_x)·s_w differs from acc·(s_x·s_w).
+    rng = np.random.default_rng(9)
+    m, k, n = 7, 1100, 13
+    codes = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    w = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    codes[0] = 127
+    codes[0, 0] = 126
+    w[:, 0] = 127                               # acc = 1100·16129 − 127 = 17 741 773: odd, past 2^24
+    sx = rng.uniform(1e-3, 1e-1, m).astype(np.float32)
+    sw = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    acc = codes.astype(np.int64) @ w.astype(np.int64)
+    expected = acc.astype(np.float32) * (sx[:, None] * sw[None, :]).astype(np.float32)
+    got = orc.w8a8_product(codes, sx, w, True, sw)
+    assert bitwise_equal(got, expected) == 0
+    assert np.array_equal(orc.w8a8_product(codes, sx, np.ascontiguousarray(w.T), False, sw), got)
+    assert acc[0, 0] == 17741773 and float(np.float32(acc[0, 0])) == 17741772.0   # the tie goes to the even
+    one = orc.w8a8_product(np.array([[1]], np.int8), np.array([0.05983570218086243], np.float32),
+                           np.array([[1]], np.int8), True, np.array([0.007420313078910112], np.float32))
+    f = np.float32
+    a = f(-284410.0) * one[0, 0]
+    assert a == f(-284410.0) * f(f(0.05983570218086243) * f(0.007420313078910112))
+    assert a != f(f(f(-284410.0) * f(0.05983570218086243)) * f(0.007420313078910112))
+    t = orc.w8a8_product(codes[:2], sx[:2], w, True, sw[:1])          # one scale for the tensor
+    assert bitwise_equal(t, acc[:2].astype(np.float32) * (sx[:2, None] * sw[0]).astype(np.float32)) == 0
