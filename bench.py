@@ -62,11 +62,17 @@ WORKLOADS = {
     "c1_convrot": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
                    "C1 up-projection on a convrot int8 weight (groups of 256): fp32 X rotated and rounded to bf16, "
                    "then the product with bias + fused GELU-tanh, bf16 out"),
+    "c1_w8a8": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
+                "C1 up-projection on the W8A8 route (ComfyUI int8_linear): fp32 X rotated (groups of 256) and quantized "
+                "per row to int8, int8 x int8 products summed in int32, float(acc)*(s_x*s_w) + bias, fused GELU-tanh, bf16 out"),
 }
 # Workloads whose weight is ComfyUI's convrot: the rotation group. Their activation is fp32 (the
 # reference's rotate_groups reads fp32, TensorGEMM.swift:181-201) and a step is the rotation pass
-# (fp32 → bf16) followed by the product — the two kernels sq8_linear_rotated runs.
-ROTATED = {"c1_convrot": 256}
+# (fp32 → bf16, or fp32 → int8 codes and row scales on the W8A8 route) followed by the product —
+# the two kernels sq8_linear_rotated / sq8_linear_quantized run.
+ROTATED = {"c1_convrot": 256, "c1_w8a8": 256}
+W8A8 = {"c1_w8a8"}
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, published
 SEEDS = {"x": 1, "w": 2, "scale": 3, "bias": 4}
 
 
@@ -274,15 +280,29 @@ def main() -> int:
         xd = torch.empty((M, K), dtype=torch.bfloat16, device=dev)   # the rotated, rounded operand
         out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
 
-        def step(marks=None):
-            if marks:
-                marks[0].record()
-            ctx.rotate(x32d, group, out=xd)
-            if marks:
-                marks[1].record()
-            ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
-            if marks:
-                marks[2].record()
+        if args.workload in W8A8:
+            codes = torch.empty((M, K), dtype=torch.int8, device=dev)
+            sx = torch.empty(M, dtype=torch.float32, device=dev)
+
+            def step(marks=None):
+                if marks:
+                    marks[0].record()
+                ctx.quantize_rows(x32d, group, codes=codes, scales=sx)
+                if marks:
+                    marks[1].record()
+                ctx.product_w8a8(codes, sx, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
+                if marks:
+                    marks[2].record()
+        else:
+            def step(marks=None):
+                if marks:
+                    marks[0].record()
+                ctx.rotate(x32d, group, out=xd)
+                if marks:
+                    marks[1].record()
+                ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
+                if marks:
+                    marks[2].record()
     elif qkv:
         outs = tuple(torch.empty((M, N // 3), dtype=torch.bfloat16, device=dev) for _ in range(3))
 
@@ -318,34 +338,39 @@ def main() -> int:
         # around each launch; the step (value) is both.
         kernel_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
         rot_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
-        rot_bytes = 4 * M * K + 2 * M * K
-        rotation = {"group": group, "ms": round(rot_ms, 5), "algorithmic_bytes": rot_bytes, "bound": "hbm",
+        rot_bytes = 4 * M * K + (1 if args.workload in W8A8 else 2) * M * K
+        rotation = {"kind": "rotate + quantize to int8" if args.workload in W8A8 else "rotate + round to bf16",
+                    "group": group, "ms": round(rot_ms, 5), "algorithmic_bytes": rot_bytes, "bound": "hbm",
                     "achieved": round(rot_bytes / (rot_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(rot_bytes / (rot_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     flops = 2.0 * M * N * K
     tflops = flops / (step_ms * 1e-3) / 1e12
     kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
-    algo_bytes = 2 * M * K + N * K + 4 * N + 4 * N + 2 * M * n_out
+    w8a8 = args.workload in W8A8
+    a_bytes = (1 * M * K + 4 * M) if w8a8 else 2 * M * K          # int8 codes + row scales, or bf16
+    algo_bytes = a_bytes + N * K + 4 * N + 4 * N + 2 * M * n_out
     intensity = flops / algo_bytes
     gbs = algo_bytes / (kernel_ms * 1e-3) / 1e9
-    if intensity >= RIDGE:
-        roofline = {"bound": "mfma", "achieved": round(kernel_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4)}
+    peak_mfma = PEAK_INT8_TOPS if w8a8 else PEAK_BF16_TFLOPS
+    if intensity >= peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9):
+        roofline = {"bound": "mfma", "achieved": round(kernel_tflops, 2), "peak": peak_mfma,
+                    "unit": "TOP/s" if w8a8 else "TFLOP/s", "frac": round(kernel_tflops / peak_mfma, 4)}
     else:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
     roofline.update({"traffic": TRAFFIC_BYTES.get((args.workload, args.layout)), "algorithmic_bytes": algo_bytes,
                      "flops": flops, "intensity_flop_per_byte": round(intensity, 1),
                      "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5),
-                     "mfma_bound_ms": round(flops / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 5)})
+                     "mfma_bound_ms": round(flops / (peak_mfma * 1e12) * 1e3, 5)})
 
     props = torch.cuda.get_device_properties(0)
     metric = ("TFLOP/s and % bf16 MFMA peak, int8-weight GEMM 4096x3072x12288 on 1 MI355X" if args.workload == "c1_up"
+              else f"TOP/s and % int8 MFMA peak, W8A8 GEMM {M}x{K}x{N} on 1 MI355X" if w8a8
               else f"TFLOP/s and % bf16 MFMA peak, {wt}-weight GEMM {M}x{K}x{N} on 1 MI355X")
     result = {
         "metric": metric,
         "value": round(tflops, 2),
-        "unit": "TFLOP/s",
+        "unit": "TOP/s" if w8a8 else "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -353,16 +378,17 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "int8" if w8a8 else "bf16",
         "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}",
         "config": {"workload": f"{args.workload}: {desc}", "M": M, "K": K, "N": N, "weight_type": wt,
                    "weight_layout": args.layout.upper(),
                    "staging_ms": None if stage_ms is None else round(stage_ms, 3), "global_batch": M,
                    "parallelism": "none (one GPU)"},
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        **({"pct_int8_peak": round(100.0 * tflops / PEAK_INT8_TOPS, 2)} if w8a8 else {}),
         "kernel_ms": round(kernel_ms, 5),
         "roofline": roofline,
-        **({"rotation": rotation} if rotation else {}),
+        **({"activation_pass": rotation} if rotation else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if not args.no_cpu:
