@@ -49,6 +49,19 @@ def test_quantize_rows_at_the_bit(gemm, orc, m, k, g):
         assert host(scales)[3] == np.float32(1e-30) and not host(codes)[3].any()
 
 
+def test_quantize_rows_known_answers(gemm, orc):
+    # Ties of rint (scale exactly 1: 63.5 → 64, −0.5 → 0, 2.5 → 2, −126.5 → −126) and the quotient
+    # whose reciprocal product rounds the other way (97 against the division's 96): the rows the
+    # oracle's own tests work by hand, here through the kernel's exact-division branch.
+    x = np.zeros((2, 8), np.float32)
+    x[0] = [127.0, 63.5, -0.5, 1.5, 2.5, 0.0, -126.5, 3.49]
+    x[1, :3] = [2.166764259338379, 1.646399736404419, -1.646399736404419]
+    codes, scales = gemm.quantize_rows(dev(x))
+    c = host(codes)
+    assert c[0].tolist() == [127, 64, 0, 2, 2, 0, -126, 3] and host(scales)[0] == 1.0
+    assert c[1, :3].tolist() == [127, 96, -96]
+
+
 def test_quantize_rows_of_a_bf16_operand(gemm, orc):
     xb = orc.normal_bf16(77, (40, 3072))
     codes, scales = gemm.quantize_rows(bf16_dev(xb), 256)
