@@ -233,6 +233,16 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
                          const float *scale, int scale_layout, const float *bias, int epilogue,
                          void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds);
 
+/* **The W8A8 fused QKV product**: sq8_linear_w8a8 of n = 3·d columns whose outputs [0,d), [d,2d),
+ * [2d,3d) go to q, k, v — row-major [m, d] (head_dim 0, leading dimension ldo) or head-major
+ * [d/head_dim, m, head_dim]; bias if given, no activation. Replaces: the fused QKV of a block whose
+ * weights take the W8A8 route (MossImage.swift:548-560, Block.swift:410-415, on submitQuantized). */
+int sq8_linear_w8a8_qkv(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx,
+                        const void *w, int w_layout, int64_t ldw,
+                        const float *scale, int scale_layout, const float *bias,
+                        void *q, void *k_out, void *v, int c_dtype, int64_t ldo, int head_dim,
+                        int m, int k, int d, double *gpu_seconds);
+
 /* ---- the elementwise passes of a DiT block around the products (all device pointers, queued) ---- */
 
 /* **Modulated RMSNorm to the next product's operand**: for each of `rows` rows of fp32 x (leading
@@ -242,6 +252,25 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
  * `modulatedNorm` of a MOSS block (MossImage.swift:399, :418). */
 int sq8_norm_modulate(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
                       const float *shift, float eps, uint16_t *out, int64_t ldo, int rows, int cols);
+
+/* **The modulated RMSNorm writing a convrot product's operand**: y = ((x·r)·w)·(1 + scale) + shift as
+ * sq8_norm_modulate computes it in fp32 (the same r, the same bits), then y·R by groups of `group`
+ * (4, 16, 64 or 256 dividing cols) rounded to bf16 into `out` — what sq8_rotate_groups writes from y,
+ * one pass instead of two; y itself into `y_out` (fp32, leading dimension ldy) unless NULL. cols a
+ * multiple of 4 up to 32 768, rows and vectors 16-byte aligned (else SQ8_EUNSUPPORTED). Replaces:
+ * the norm then rotate_groups and round_bf16 before a convrot product (ElementwiseGPUMoss.swift:45-91,
+ * TensorGEMMBF16.swift:222-233); the producer-rounded operand (WeightProducts.swift:130-229). */
+int sq8_norm_modulate_rotated(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                              const float *shift, float eps, int group, uint16_t *out, int64_t ldo,
+                              float *y_out, int64_t ldy, int rows, int cols);
+
+/* **The modulated RMSNorm writing a W8A8 product's operand**: y as above, rotated by `group` (0: none)
+ * and quantized per row into codes int8 [rows, ldq] and scales fp32 [rows] — sq8_quantize_rows's bits
+ * on y; y into `y_out` unless NULL. Same limits. Replaces: `norm_modulate_quantized`
+ * (ElementwiseGPUMoss.swift:94-130) writing `RoundedOperand.int8` (WeightProducts.swift:144-229). */
+int sq8_norm_modulate_quantized(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                                const float *shift, float eps, int group, int8_t *codes, int64_t ldq,
+                                float *scales, float *y_out, int64_t ldy, int rows, int cols);
 
 /* **Per-row RMSNorm in place** of bf16 rows of `cols` ≤ 256 values (the heads of q or k):
  * t = bf16((t·r)·w), r = 1/sqrt(mean(t²) + eps), w fp32 [cols]. Replaces: the per-head RMSNorm of

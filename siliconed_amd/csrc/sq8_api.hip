@@ -262,7 +262,7 @@ struct W8A8 {
     const int8_t *codes; int64_t ldq; const float *sx;       // else these
     const void *w; int w_layout; int64_t ldw;
     const float *scale; int scale_layout; const float *bias; int epilogue;
-    void *c; int c_dtype; int64_t ldc;
+    void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
     int m, k, n;
 };
 
@@ -280,10 +280,10 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     if (gpu_seconds) *gpu_seconds = 0.0;
     if (q.m == 0 || n_out == 0) return SQ8_OK;
     if (q.k == 0) return SQ8_EUNSUPPORTED;
-    if (!q.w || !q.scale || !q.c) return SQ8_EINVAL;
+    if (!q.w || !q.scale || !q.c[0]) return SQ8_EINVAL;
     if (q.a ? q.lda < q.k : (!q.codes || !q.sx || q.ldq < q.k)) return SQ8_EINVAL;
     if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
-    if (q.ldc < n_out) return SQ8_EINVAL;
+    if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
     const int k_pad = (q.k + 127) / 128 * 128;
     // The kernel addresses the codes and the weight with 32-bit byte offsets from their bases.
     if ((int64_t)q.m * std::max<int64_t>(k_pad, q.ldq) > (int64_t)UINT32_MAX ||
@@ -324,16 +324,31 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     p.sx = sx;
     p.scale = q.scale;
     p.bias = q.bias;
-    p.c[0] = q.c;
+    p.c[0] = q.c[0];
+    p.c[1] = q.c[1];
+    p.c[2] = q.c[2];
+    if (q.split > 0) {
+        p.c_d1 = (int64_t)((uintptr_t)q.c[1] - (uintptr_t)q.c[0]);
+        p.c_d2 = (int64_t)((uintptr_t)q.c[2] - (uintptr_t)q.c[0]);
+    }
     p.ldc = q.ldc;
+    p.split = q.split;
+    p.head_dim = q.head_dim;
     p.M = q.m;
     p.N = q.n;
     p.K = q.k;
     p.glu_half = is_glu(q.epilogue) ? q.n / 2 : 0;
     p.scale_per_col = q.scale_layout == SQ8_SCALE_COLUMNS;
     const size_t esz = q.c_dtype == SQ8_F32 ? 4 : 2;
-    p.c_vec = aligned(q.c, 4 * esz) && (q.ldc % 4) == 0;
-    p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
+    // 16-byte stores: 8 bf16 / 4 fp32 columns that never straddle a split or a head.
+    const int per16 = (int)(16 / esz);
+    bool cv16 = true;
+    for (int i = 0; i < (q.split > 0 ? 3 : 1); ++i) cv16 = cv16 && aligned(q.c[i], 16);
+    if (q.split > 0) cv16 = cv16 && (q.split % per16) == 0;
+    if (q.head_dim > 0) cv16 = cv16 && (q.head_dim % per16) == 0;
+    else cv16 = cv16 && (q.ldc % per16) == 0;
+    p.c_vec16 = cv16;
+    p.c_vec = cv16;
     p.sb_vec = aligned(q.scale, 16) && (!q.bias || aligned(q.bias, 16)) && (p.glu_half % 4) == 0;
     p.kt = k_pad / 128;
     // The weight: packed as staged, [N, K] read in place when its rows hold whole steps, else
@@ -536,9 +551,57 @@ int sq8_linear_w8a8(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float 
     q.codes = codes; q.ldq = ldq; q.sx = sx;
     q.w = w; q.w_layout = w_layout; q.ldw = ldw;
     q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
-    q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
     q.m = m; q.k = k; q.n = n;
     return run_w8a8(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_w8a8_qkv(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx, const void *w, int w_layout,
+                        int64_t ldw, const float *scale, int scale_layout, const float *bias, void *q_out, void *k_out,
+                        void *v_out, int c_dtype, int64_t ldo, int head_dim, int m, int k, int d, double *gpu_seconds) {
+    if (d < 0 || (d % 4) != 0 || head_dim < 0) return SQ8_EINVAL;
+    if (head_dim > 0 && ((d % head_dim) != 0 || (head_dim % 4) != 0)) return SQ8_EINVAL;
+    if (head_dim == 0 && ldo < d) return SQ8_EINVAL;
+    if (d > 0 && (!q_out || !k_out || !v_out)) return SQ8_EINVAL;
+    if ((int64_t)3 * d > INT32_MAX) return SQ8_EINVAL;
+    W8A8 q;
+    memset(&q, 0, sizeof(q));
+    q.codes = codes; q.ldq = ldq; q.sx = sx;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = SQ8_EPI_NONE;
+    q.c[0] = q_out; q.c[1] = k_out; q.c[2] = v_out; q.c_dtype = c_dtype; q.ldc = ldo;
+    q.split = d; q.head_dim = head_dim;
+    q.m = m; q.k = k; q.n = 3 * d;
+    return run_w8a8(ctx, q, gpu_seconds);
+}
+
+int sq8_norm_modulate_rotated(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                              const float *shift, float eps, int group, uint16_t *out, int64_t ldo, float *y_out,
+                              int64_t ldy, int rows, int cols) {
+    if (!ctx || rows < 0 || cols < 0) return SQ8_EINVAL;
+    if (!sq8::is_rotation_group(group) || cols % group != 0) return SQ8_EINVAL;
+    if (rows == 0 || cols == 0) return SQ8_OK;
+    if (!x || !w || !scale || !shift || !out || ldx < cols || ldo < cols || (y_out && ldy < cols)) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    const hipError_t e = sq8::launch_norm_operand(x, ldx, w, scale, shift, eps, rows, cols, group, y_out, ldy, out, ldo,
+                                                  nullptr, 0, 0, nullptr, ctx->stream);
+    return e == hipErrorInvalidValue ? SQ8_EUNSUPPORTED : hip_status(e);
+}
+
+int sq8_norm_modulate_quantized(sq8_ctx *ctx, const float *x, int64_t ldx, const float *w, const float *scale,
+                                const float *shift, float eps, int group, int8_t *codes, int64_t ldq, float *scales,
+                                float *y_out, int64_t ldy, int rows, int cols) {
+    if (!ctx || rows < 0 || cols < 0) return SQ8_EINVAL;
+    if (group != 0 && (!sq8::is_rotation_group(group) || cols % group != 0)) return SQ8_EINVAL;
+    if (rows == 0 || cols == 0) return SQ8_OK;
+    if (!x || !w || !scale || !shift || !codes || !scales || ldx < cols || ldq < cols || (y_out && ldy < cols))
+        return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    const hipError_t e = sq8::launch_norm_operand(x, ldx, w, scale, shift, eps, rows, cols, group, y_out, ldy, nullptr, 0,
+                                                  codes, ldq, cols, scales, ctx->stream);
+    return e == hipErrorInvalidValue ? SQ8_EUNSUPPORTED : hip_status(e);
 }
 
 int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group, const void *w, int w_layout,
@@ -550,7 +613,7 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
     q.a = a; q.a_dtype = a_dtype; q.lda = lda; q.group = group;
     q.w = w; q.w_layout = w_layout; q.ldw = ldw;
     q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
-    q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
     q.m = m; q.k = k; q.n = n;
     if (!a) return m == 0 ? SQ8_OK : SQ8_EINVAL;
     return run_w8a8(ctx, q, gpu_seconds);

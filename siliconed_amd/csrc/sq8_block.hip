@@ -8,6 +8,8 @@
 
 #include "sq8_device.h"
 #include "sq8_gemm.h"
+#include "sq8_quant.h"
+#include "sq8_rotate.h"
 
 namespace sq8 {
 namespace {
@@ -60,6 +62,102 @@ __global__ void __launch_bounds__(256) norm_modulate_kernel(const float *__restr
         }
     } else {
         for (int i = threadIdx.x; i < cols; i += 256) dst[i] = round_bf16(one(src[i], i));
+    }
+}
+
+// The modulated RMSNorm writing the next product's operand itself (the reference's
+// `norm_modulate_quantized`, ElementwiseGPUMoss.swift:94-130, and the operand contract of
+// WeightProducts.swift:130-229): y — the fp32 row norm_modulate_kernel<true> computes, the same r
+// (its summation order) and the same operations, hence the same bits — is rotated by `stages` stages
+// (a convrot weight) and then rounded to bf16 (ROT: what sq8_rotate_groups writes from y) or
+// quantized per row (Q8: what sq8_quantize_rows writes from y). y is also written where `y_out` is
+// given. The row is held as rot::rotate_chunk holds it, wave w taking the quads w, w + 4, …
+// (IT of them at most). cols % 4 == 0 and 16-byte aligned rows and vectors (the launcher checks).
+constexpr int OP_ROT = 0, OP_Q8 = 1;
+
+template <int MODE, int IT>
+__global__ void __launch_bounds__(256) norm_operand_kernel(const float *__restrict__ x, int64_t ldx, const float *__restrict__ w,
+                                                           const float *__restrict__ scale, const float *__restrict__ shift,
+                                                           float eps, int cols, int stages, float norm, float *y_out,
+                                                           int64_t ldy, uint16_t *out, int64_t ldo, int8_t *codes,
+                                                           int64_t ldq, int k_pad, float *scales) {
+    __shared__ float partial[4];
+    __shared__ __attribute__((aligned(16))) float lds[4][4 * rot::PITCH];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int cc = lane >> 4, l16 = lane & 15;
+    float *mine = lds[wave] + cc * rot::PITCH;
+    const int64_t row = blockIdx.x;
+    const float *src = x + row * ldx;
+    // r exactly as norm_modulate_kernel<true>: 16-byte loads at 4t + 1024j, then the block sum.
+    float ss = 0.0f;
+    for (int i = 4 * threadIdx.x; i < cols; i += 1024) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(src + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss = __fadd_rn(ss, __fmul_rn(v[e], v[e]));
+    }
+    const float mean = __fdiv_rn(block_sum_256(ss, partial), (float)cols);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    const int cpr = (cols + 255) / 256;
+    float v[IT][16];
+    float m = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int quad = it * 4 + wave;
+        if (4 * quad >= cpr) break;  // wave-uniform
+        const int chunk = 4 * quad + cc;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int col = chunk * 256 + 4 * l16 + 64 * u;
+            if (chunk < cpr && col < cols) {
+                const f32x4 xv = *reinterpret_cast<const f32x4 *>(src + col);
+                const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + col);
+                const f32x4 sv = *reinterpret_cast<const f32x4 *>(scale + col);
+                const f32x4 hv = *reinterpret_cast<const f32x4 *>(shift + col);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float t = __fmul_rn(__fmul_rn(xv[e], r), wv[e]);
+                    v[it][4 * u + e] = __fadd_rn(__fmul_rn(t, __fadd_rn(sv[e], 1.0f)), hv[e]);
+                }
+                if (y_out)
+                    *reinterpret_cast<f32x4 *>(y_out + row * ldy + col) =
+                        f32x4{v[it][4 * u], v[it][4 * u + 1], v[it][4 * u + 2], v[it][4 * u + 3]};
+            } else {
+                v[it][4 * u] = v[it][4 * u + 1] = v[it][4 * u + 2] = v[it][4 * u + 3] = 0.0f;
+            }
+        }
+        rot::rotate_chunk(v[it], mine, l16, stages);
+        if constexpr (MODE == OP_ROT) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int col = chunk * 256 + 4 * l16 + 64 * u;
+                if (chunk < cpr && col < cols) {
+                    float t[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = v[it][4 * u + e] * norm;
+                    *reinterpret_cast<u32x2 *>(out + row * ldo + col) =
+                        u32x2{round_bf16(t[0]) | round_bf16(t[1]) << 16, round_bf16(t[2]) | round_bf16(t[3]) << 16};
+                }
+            }
+        } else {
+            m = quant::scaled_max(v[it], norm, m);
+        }
+    }
+    if constexpr (MODE == OP_Q8) {
+        // The row's maximum (exact in any order), its scale, the codes (sq8_quantize_rows's code).
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        __syncthreads();  // every thread has read the sum out of partial[] before it is reused
+        if (lane == 0) partial[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
+        const float sc = quant::row_scale(m);
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int quad = it * 4 + wave;
+            if (4 * quad >= cpr) break;
+            quant::store_codes<true>(codes + row * ldq, cols, k_pad, 4 * quad + cc, cpr, l16, v[it], sc);
+        }
+        if (threadIdx.x == 0) scales[row] = sc;
     }
 }
 
@@ -148,6 +246,33 @@ hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, con
         hipLaunchKernelGGL(norm_modulate_kernel<false>, dim3(rows), dim3(256), 0, stream, x, ldx, w, scale, shift, eps, out,
                            ldo, cols);
     return hipGetLastError();
+}
+
+hipError_t launch_norm_operand(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,
+                               float eps, int rows, int cols, int group, float *y_out, int64_t ldy, uint16_t *out,
+                               int64_t ldo, int8_t *codes, int64_t ldq, int k_pad, float *scales, hipStream_t stream) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    auto a16 = [](const void *q) { return q == nullptr || (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool q8 = codes != nullptr;
+    if (cols % 4 || ldx % 4 || !a16(x) || !a16(w) || !a16(scale) || !a16(shift) || (y_out && (ldy % 4 || !a16(y_out))) ||
+        (!q8 && (ldo % 4 || (reinterpret_cast<uintptr_t>(out) & 7))) ||
+        (q8 && (ldq % 4 || (reinterpret_cast<uintptr_t>(codes) & 3) || k_pad % 4 || k_pad < cols)) ||
+        cols > 8 * 4096)
+        return hipErrorInvalidValue;
+    const int stages = rot::stages_of(group);
+    const float norm = group > 0 ? 1.0f / sqrtf((float)group) : 1.0f;
+    const int quads = (cols + 1023) / 1024;
+    const int it = quads <= 4 ? 1 : quads <= 8 ? 2 : quads <= 16 ? 4 : 8;
+#define SQ8_NO(MD, I)                                                                                               \
+    if ((q8 ? OP_Q8 : OP_ROT) == MD && it == I) {                                                                     \
+        hipLaunchKernelGGL((norm_operand_kernel<MD, I>), dim3(rows), dim3(256), 0, stream, x, ldx, w, scale, shift, eps, \
+                           cols, stages, norm, y_out, ldy, out, ldo, codes, ldq, k_pad, scales);                      \
+        return hipGetLastError();                                                                                     \
+    }
+    SQ8_NO(OP_ROT, 1) SQ8_NO(OP_ROT, 2) SQ8_NO(OP_ROT, 4) SQ8_NO(OP_ROT, 8)
+    SQ8_NO(OP_Q8, 1) SQ8_NO(OP_Q8, 2) SQ8_NO(OP_Q8, 4) SQ8_NO(OP_Q8, 8)
+#undef SQ8_NO
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_rms_rows(uint16_t *t, int64_t ld, int64_t rows, int cols, const float *w, float eps, hipStream_t stream) {

@@ -91,6 +91,12 @@ hipError_t launch_i8gemm(const GemmArgs &p, int wl, int epi, int out, hipStream_
 // The DiT block's elementwise passes (sq8_block.hip).
 hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,
                                 float eps, uint16_t *out, int64_t ldo, int rows, int cols, hipStream_t stream);
+// The modulated RMSNorm writing the next product's operand: y rotated by `group` (0: none) and
+// rounded to bf16 into `out` (codes == nullptr), or quantized per row into codes (rows of k_pad) and
+// scales; y itself into y_out when given. cols % 4 == 0, 16-byte aligned rows and vectors, cols ≤ 32 768.
+hipError_t launch_norm_operand(const float *x, int64_t ldx, const float *w, const float *scale, const float *shift,
+                               float eps, int rows, int cols, int group, float *y_out, int64_t ldy, uint16_t *out,
+                               int64_t ldo, int8_t *codes, int64_t ldq, int k_pad, float *scales, hipStream_t stream);
 hipError_t launch_rms_rows(uint16_t *t, int64_t ld, int64_t rows, int cols, const float *w, float eps, hipStream_t stream);
 hipError_t launch_gated_residual(float *x, int64_t ldx, const void *y, bool y_bf16, int64_t ldy, const float *gate,
                                  int64_t rows, int cols, hipStream_t stream);

@@ -409,6 +409,73 @@ class TensorGEMM:
         abi.check(st, "sq8_norm_modulate")
         return out
 
+    def _norm_args(self, x, w, scale, shift, y_out):
+        if x.dtype != torch.float32 or x.dim() != 2:
+            raise ValueError("x must be fp32 [rows, cols]")
+        rows, cols = x.shape
+        for t, name in ((w, "w"), (scale, "scale"), (shift, "shift")):
+            if t.dtype != torch.float32 or t.numel() != cols or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous fp32 [cols]")
+        if y_out is not None and (y_out.dtype != torch.float32 or tuple(y_out.shape) != (rows, cols)):
+            raise ValueError("y_out must be fp32 [rows, cols]")
+        return rows, cols
+
+    def norm_modulate_rotated(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                              eps: float, group: int, *, out: Optional[torch.Tensor] = None,
+                              y_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The modulated RMSNorm's row y, rotated by `group` and rounded to bf16: a convrot product's
+        operand in one pass (y itself into `y_out` when given)."""
+        rows, cols = self._norm_args(x, w, scale, shift, y_out)
+        if out is None:
+            out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
+        st = abi.load().sq8_norm_modulate_rotated(
+            self._h, _dev(x, "x"), _row_major(x, "x"), _dev(w, "w"), _dev(scale, "scale"), _dev(shift, "shift"), eps,
+            int(group), _dev(out, "out"), _row_major(out, "out"),
+            None if y_out is None else _dev(y_out, "y_out"), 0 if y_out is None else _row_major(y_out, "y_out"), rows, cols)
+        abi.check(st, "sq8_norm_modulate_rotated")
+        return out
+
+    def norm_modulate_quantized(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                                eps: float, group: int = 0, *, codes: Optional[torch.Tensor] = None,
+                                scales: Optional[torch.Tensor] = None, y_out: Optional[torch.Tensor] = None):
+        """The modulated RMSNorm's row y, rotated by `group` (0: none) and quantized per row: a W8A8
+        product's operand (codes int8 [rows, cols], scales fp32 [rows]) in one pass."""
+        rows, cols = self._norm_args(x, w, scale, shift, y_out)
+        if codes is None:
+            codes = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+        if scales is None:
+            scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+        st = abi.load().sq8_norm_modulate_quantized(
+            self._h, _dev(x, "x"), _row_major(x, "x"), _dev(w, "w"), _dev(scale, "scale"), _dev(shift, "shift"), eps,
+            int(group), _dev(codes, "codes"), _row_major(codes, "codes"), _dev(scales, "scales"),
+            None if y_out is None else _dev(y_out, "y_out"), 0 if y_out is None else _row_major(y_out, "y_out"), rows, cols)
+        abi.check(st, "sq8_norm_modulate_quantized")
+        return codes, scales
+
+    def product_w8a8_qkv(self, codes: torch.Tensor, sx: torch.Tensor, w, scale: torch.Tensor, *,
+                         bias: Optional[torch.Tensor] = None, head_dim: int = 0, out=None,
+                         out_dtype: torch.dtype = torch.bfloat16):
+        """The W8A8 fused QKV: (q, k, v), each [m, d] (head_dim 0) or [d/head_dim, m, head_dim]."""
+        m, k = codes.shape
+        if isinstance(w, PackedWeight):
+            lay, n, ldw, wptr = w.layout, w.n, w.k, _dev(w.data, "w")
+        else:
+            lay, n, ldw, wptr = abi.NK, w.shape[0], _row_major(w, "w"), _dev(w, "w")
+        if n % 3:
+            raise ValueError("a fused QKV weight has 3·d columns")
+        d = n // 3
+        shape = (m, d) if head_dim == 0 else (d // head_dim, m, head_dim)
+        if out is None:
+            out = tuple(torch.empty(shape, dtype=out_dtype, device=codes.device) for _ in range(3))
+        per_col = scale.numel() != 1
+        st = abi.load().sq8_linear_w8a8_qkv(
+            self._h, _dev(codes, "codes"), _row_major(codes, "codes"), _dev(sx, "sx"), wptr, lay, ldw,
+            _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"), _dev(out[0], "q"), _dev(out[1], "k"), _dev(out[2], "v"),
+            _cdtype(out_dtype), d if head_dim == 0 else 0, head_dim, m, k, d, None)
+        abi.check(st, "sq8_linear_w8a8_qkv")
+        return out
+
     def rms_rows(self, t: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
         """In place: each row of the bf16 tensor t (last dimension ≤ 256, rows contiguous) →
         bf16((t·r)·w) — the per-head RMSNorm of q and k."""

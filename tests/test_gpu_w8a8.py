@@ -201,3 +201,75 @@ def test_linear_mirror_quantizing(gemm, orc):
     gemm.linear(dev(x), int8=dev(q_kn).view(torch.int8), scales=dev(sw), per_column=True, c=c2, m=m, k=k, n=n,
                 prequantized=(dev(codes), dev(sx)))
     assert bitwise_equal(host(c2), expected) == 0
+
+
+# ---- the operand written by its producer (WeightProducts.swift:130-229, ElementwiseGPUMoss.swift:94-130) ----
+
+def _norm_inputs(orc, rows, cols, seed):
+    x = orc.normal_f32(seed, (rows, cols), 0.0, 2.0)
+    w = (1.0 + 0.05 * orc.normal_f32(seed + 1, (cols,))).astype(np.float32)
+    sc = (0.1 * orc.normal_f32(seed + 2, (cols,))).astype(np.float32)
+    sh = (0.1 * orc.normal_f32(seed + 3, (cols,))).astype(np.float32)
+    return x, w, sc, sh
+
+
+@pytest.mark.parametrize("rows,cols,g", [(300, 3072, 256), (5, 1024, 0), (33, 5120, 64), (7, 12288, 256), (3, 20480, 16)])
+def test_norm_writes_the_w8a8_operand(gemm, orc, rows, cols, g):
+    # y is the fp32 row of sq8_norm_modulate (its bf16 rounding equals that pass's output, bit for bit);
+    # the codes and scales are sq8_quantize_rows's on y (the oracle's, bit for bit); without y_out the same.
+    x, w, sc, sh = _norm_inputs(orc, rows, cols, rows + cols + g)
+    xd, wd, scd, shd = dev(x), dev(w), dev(sc), dev(sh)
+    y = torch.empty((rows, cols), dtype=torch.float32, device=DEV)
+    codes, scales = gemm.norm_modulate_quantized(xd, wd, scd, shd, 1e-6, g, y_out=y)
+    yh = host(y)
+    plain = gemm.norm_modulate(xd, wd, scd, shd, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(plain.cpu().view(torch.int16).numpy().view(np.uint16), orc.f32_to_bf16(yh))
+    ec, es = orc.quantize_rows(yh, g)
+    assert np.array_equal(host(codes), ec) and bitwise_equal(host(scales), es) == 0
+    c2, s2 = gemm.norm_modulate_quantized(xd, wd, scd, shd, 1e-6, g)
+    assert np.array_equal(host(c2), ec) and bitwise_equal(host(s2), es) == 0
+
+
+@pytest.mark.parametrize("rows,cols,g", [(300, 3072, 256), (9, 1024, 16), (4, 12288, 64)])
+def test_norm_writes_the_convrot_operand(gemm, orc, rows, cols, g):
+    # The rotated, rounded operand is the rotation pass's on y (the oracle's rotation, bit for bit).
+    x, w, sc, sh = _norm_inputs(orc, rows, cols, rows * 7 + g)
+    y = torch.empty((rows, cols), dtype=torch.float32, device=DEV)
+    out = gemm.norm_modulate_rotated(dev(x), dev(w), dev(sc), dev(sh), 1e-6, g, y_out=y)
+    torch.cuda.synchronize()
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, orc.f32_to_bf16(orc.rotate_groups(host(y), g)))
+    out2 = gemm.norm_modulate_rotated(dev(x), dev(w), dev(sc), dev(sh), 1e-6, g)
+    torch.cuda.synchronize()
+    assert np.array_equal(out2.cpu().view(torch.int16).numpy().view(np.uint16), got)
+
+
+def test_norm_operand_refusals(gemm, orc):
+    from siliconed_amd import abi
+    x, w, sc, sh = (dev(a) for a in _norm_inputs(orc, 2, 96, 1))
+    with pytest.raises(abi.SQ8Error):
+        gemm.norm_modulate_quantized(x, w, sc, sh, 1e-6, 64)        # 96 is no whole number of groups of 64
+    with pytest.raises(abi.SQ8Error):
+        gemm.norm_modulate_rotated(x, w, sc, sh, 1e-6, 0)           # a rotation needs a group
+    xs = torch.zeros((2, 98), device=DEV)
+    with pytest.raises(abi.Unsupported):
+        gemm.norm_modulate_quantized(xs, xs[0].contiguous(), xs[0].contiguous(), xs[0].contiguous(), 1e-6)  # cols % 4
+
+
+@pytest.mark.parametrize("head_dim", [0, 128])
+def test_w8a8_qkv_is_the_split_product(gemm, orc, head_dim):
+    m, k, d = 300, 1024, 512
+    x = inputs(orc, m, k, 61)
+    q = orc.uniform_i8(62, (3 * d, k))
+    sw = orc.uniform_f32(63, (3 * d,), 1e-3, 2e-2)
+    b = orc.normal_f32(64, (3 * d,), 0.0, 0.02)
+    codes, sx = orc.quantize_rows(x, 256)
+    w = gemm.pack(dev(q).view(torch.int8), layout="nk")
+    full = host(gemm.product_w8a8(dev(codes), dev(sx), w, dev(sw), bias=dev(b)).float())
+    outs = gemm.product_w8a8_qkv(dev(codes), dev(sx), w, dev(sw), bias=dev(b), head_dim=head_dim)
+    for i, t in enumerate(outs):
+        part = host(t.float())
+        if head_dim:
+            part = part.transpose(1, 0, 2).reshape(m, d)
+        assert np.array_equal(part, full[:, i * d:(i + 1) * d]), i
