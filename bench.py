@@ -175,7 +175,8 @@ def dit_block(args) -> int:
     import torch
     from siliconed_amd.dit_block import DiTBlock
     S, d, heads = 4096 + 512, 3072, 24
-    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=SEEDS["w"])
+    w8a8 = args.workload == "c4_block_w8a8"
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=SEEDS["w"], route="w8a8" if w8a8 else "bf16", group=256 if w8a8 else 0)
     x = torch.from_numpy(normal_f32(SEEDS["x"], S * d).reshape(S, d)).cuda()
     temb = torch.from_numpy(normal_f32(SEEDS["bias"], d)).cuda()
     steps = max(args.steps // 5, 5)
@@ -197,13 +198,17 @@ def dit_block(args) -> int:
     flops = blk.flops(S)
     tflops = flops / (ms * 1e-3) / 1e12
     result = {
-        "metric": "DiT block forward ms (hidden 3072, 24x128 heads, 4608 tokens, int8 weights) on 1 MI355X",
+        "metric": ("DiT block forward ms (hidden 3072, 24x128 heads, 4608 tokens, int8 weights"
+                   + (", W8A8 route, convrot 256" if w8a8 else "") + ") on 1 MI355X"),
         "value": round(tflops, 2), "unit": "TFLOP/s", "block_ms": round(ms, 4), "n_gpus": 1, "steps": steps,
         "warmup": max(args.warmup // 20, 5), "ms_per_step": round(1e3 * wall / steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": f"synthetic, seeded: x, temb SplitMix64 + Box-Muller; weights torch generator seed {SEEDS['w']}",
-        "config": {"workload": "c4_block: one single-stream DiT block (modulation, modulated RMSNorm, fused QKV, "
-                               "per-head RMSNorm, SDPA, Wo, GELU MLP 4x, gated residuals)", "tokens": S, "hidden": d, "heads": heads,
+        "config": {"workload": f"{args.workload}: one single-stream DiT block (modulation, modulated RMSNorm, fused QKV, "
+                               "per-head RMSNorm, SDPA, Wo, GELU MLP 4x, gated residuals)"
+                               + ("; products W8A8 (int8 activations quantized per row after a convrot rotation of 256, "
+                                  "the norms writing the QKV and W_up codes)" if w8a8 else ""),
+                   "tokens": S, "hidden": d, "heads": heads,
                    "flops": flops, "global_batch": S, "parallelism": "none (one GPU)"},
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
     }
@@ -218,7 +223,7 @@ def main() -> int:
     # The clocks reach their steady state only after ~50 ms of sustained work: 10 warm-up steps leave
     # the first timed steps 30 % slow (0.36 ms against 0.27 ms each on the default workload).
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4_block"], default="c1_up")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4_block", "c4_block_w8a8"], default="c1_up")
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -245,7 +250,7 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": nbytes, "launches": args.steps}), flush=True)
         return 0
 
-    if args.workload == "c4_block":
+    if args.workload in ("c4_block", "c4_block_w8a8"):
         return dit_block(args)
     M, K, N, wt, epi, _, desc = WORKLOADS[args.workload]
     fp8 = wt == "fp8"

@@ -9,6 +9,12 @@ One block of MossImage.swift:15-19 with the 4× GELU-tanh MLP of the other DiT t
 
 with the six modulation vectors [shift_a, scale_a, gate_a, shift_f, scale_f, gate_f] from one Linear
 of the timestep embedding (MossImage.swift:23-27: no SiLU before it, the shift first, plain gates).
+
+`route="w8a8"`: the block's products on the W8A8 route (ComfyUI's int8_linear,
+TensorGEMMInt8.swift:4-37) with convrot weights of rotation group `group` (0: none): the norms write
+the QKV and W_up operands as int8 codes themselves (sq8_norm_modulate_quantized, the reference's
+norm_modulate_quantized), the attention output and the GELU output are quantized by the quantization
+pass, and every product but the modulation's (one row: the bf16 route's skinny kernel) is int8 × int8.
 Every Linear — the modulation, the fused QKV, Wo, W_up (GELU fused) and W_down — is an int8
 per-output-channel product of this library (weights w ~ N(0, 0.02), s = amax/127,
 q = clamp(rint(w/s), −127, 127), staged once in the packed layout). The residual stream is fp32 as
@@ -33,10 +39,13 @@ def quantize_int8(w: torch.Tensor):
     return q, s.float()
 
 
-def rms_modulate(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
-    """RMS(x)·w·(1 + scale) + shift, fp32 arithmetic, bf16 result (the next product's operand)."""
+def rms_modulate(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                 to_bf16: bool = True) -> torch.Tensor:
+    """RMS(x)·w·(1 + scale) + shift, fp32 arithmetic; rounded to bf16 (the next product's operand on
+    the bf16 route) unless `to_bf16` is false (the W8A8 route quantizes the fp32 row)."""
     r = torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + EPS)
-    return ((x * r) * w * (1.0 + scale) + shift).to(torch.bfloat16)
+    y = (x * r) * w * (1.0 + scale) + shift
+    return y.to(torch.bfloat16) if to_bf16 else y
 
 
 def rms_heads(t: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -56,9 +65,12 @@ class DiTBlock:
     """The block's weights (int8 packed, fp32 scales, fp32 norm weights) on one device."""
 
     def __init__(self, d: int = 3072, heads: int = 24, mlp: int = 4, seed: int = 0, device: int = 0,
-                 ctx: TensorGEMM | None = None):
+                 ctx: TensorGEMM | None = None, route: str = "bf16", group: int = 0):
         if d % heads or (d // heads) % 8:
             raise ValueError("d must split into heads of a multiple of 8")
+        if route not in ("bf16", "w8a8"):
+            raise ValueError("route is 'bf16' or 'w8a8'")
+        self.route, self.group = route, group
         self.d, self.heads, self.hd = d, heads, d // heads
         self.ctx = ctx or context(device)
         dev = torch.device("cuda", device)
@@ -83,12 +95,36 @@ class DiTBlock:
     def _product(self, x: torch.Tensor, lin: dict, epilogue=None, out_dtype=torch.bfloat16) -> torch.Tensor:
         return self.ctx.product(x, lin["packed"], lin["s"], bias=lin["b"], epilogue=epilogue, out_dtype=out_dtype)
 
+    def _product8(self, codes_sx, lin: dict, epilogue=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+        codes, sx = codes_sx
+        return self.ctx.product_w8a8(codes, sx, lin["packed"], lin["s"], bias=lin["b"], epilogue=epilogue,
+                                     out_dtype=out_dtype)
+
+    def _forward_w8a8(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
+        S, d = x.shape
+        ctx, g = self.ctx, self.group
+        mod = self._product(temb.to(torch.bfloat16)[None], self.mod, out_dtype=torch.float32)[0]
+        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
+        n8 = ctx.norm_modulate_quantized(x, self.norm_a, scale_a, shift_a, EPS, g)
+        q, k, v = ctx.product_w8a8_qkv(n8[0], n8[1], self.qkv["packed"], self.qkv["s"], bias=self.qkv["b"])
+        ctx.rms_rows(q.view(S * self.heads, self.hd), self.norm_q, EPS)
+        ctx.rms_rows(k.view(S * self.heads, self.hd), self.norm_k, EPS)
+        heads = lambda t: t.view(S, self.heads, self.hd).transpose(0, 1)
+        o = attention(heads(q), heads(k), heads(v)).transpose(0, 1).reshape(S, d)
+        ctx.gated_residual(x, self._product8(ctx.quantize_rows(o, g), self.out), gate_a)
+        m8 = ctx.norm_modulate_quantized(x, self.norm_f, scale_f, shift_f, EPS, g)
+        h = self._product8(m8, self.up, epilogue="gelu_tanh")
+        ctx.gated_residual(x, self._product8(ctx.quantize_rows(h, g), self.down), gate_f)
+        return x
+
     def forward_(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
         """The block on the residual stream x (fp32 [S, d], contiguous), updated in place as the
         reference's stream buffer is; temb [d]. Every pass but the attention is this library's: the
         modulation, the fused QKV (rows [S, heads·hd]: q, k, v are [heads, S, hd] views), Wo, W_up with
         GELU fused and W_down products; the modulated norms, the per-head norms of q and k and the
         gated residual updates."""
+        if self.route == "w8a8":
+            return self._forward_w8a8(x, temb)
         S, d = x.shape
         ctx = self.ctx
         mod = self._product(temb.to(torch.bfloat16)[None], self.mod, out_dtype=torch.float32)[0]
@@ -109,23 +145,45 @@ class DiTBlock:
         """x fp32 [S, d] (the residual stream), temb [d]: the block's output, fp32 [S, d] (x kept)."""
         return self.forward_(x.clone(), temb)
 
+    def _rotate(self, a: torch.Tensor) -> torch.Tensor:
+        """a·R by groups of `group` in fp32 (R = H/√G, H the Kronecker power of the regular H4)."""
+        g = self.group
+        if not g:
+            return a
+        h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float32, device=a.device)
+        h = torch.ones((1, 1), device=a.device)
+        while h.shape[0] < g:
+            h = torch.kron(h, h4)
+        return (a.reshape(a.shape[0], -1, g) @ (h / g ** 0.5)).reshape(a.shape)
+
+    def _quantized(self, a: torch.Tensor) -> torch.Tensor:
+        """The W8A8 operand in fp32: a rotated, quantized per row (s = max|y|/127, rint) and scaled back."""
+        y = self._rotate(a.float())
+        s = (y.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(1e-30)
+        return torch.round(y / s).clamp(-128, 127) * s
+
     def reference(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
         """The same block in fp32 with the dequantised weights (Float(q)·s) and fp32 math attention:
-        the check of `forward` (operands rounded to bf16 where `forward` rounds them)."""
-        def lin(a, L, act=None):
-            y = a.float() @ (L["q"].float() * L["s"][:, None]).t() + L["b"]
+        the check of `forward` (operands rounded to bf16 where `forward` rounds them; on the W8A8
+        route quantized per row after the rotation, as `forward` quantizes them — the product of a
+        rotated operand with the stored weight is the product with the convrot weight (q·s)·R)."""
+        def lin(a, L, act=None, w8=None):
+            w8 = self.route == "w8a8" if w8 is None else w8
+            a = self._quantized(a) if w8 else a.float()
+            y = a @ (L["q"].float() * L["s"][:, None]).t() + L["b"]
             return torch.nn.functional.gelu(y, approximate="tanh") if act else y
         S, d = x.shape
-        mod = lin(temb.to(torch.bfloat16)[None], self.mod)[0]
+        mod = lin(temb.to(torch.bfloat16)[None], self.mod, w8=False)[0]
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
-        n = rms_modulate(x, self.norm_a, scale_a, shift_a)
+        w8 = self.route == "w8a8"
+        n = rms_modulate(x, self.norm_a, scale_a, shift_a, to_bf16=not w8)
         qkv = lin(n, self.qkv).to(torch.bfloat16).view(S, 3, self.heads, self.hd).permute(1, 2, 0, 3)
         q, k, v = (rms_heads(t.contiguous(), w).float() if w is not None else t.float()
                    for t, w in zip(qkv, (self.norm_q, self.norm_k, None)))
         att = torch.softmax((q @ k.transpose(1, 2).contiguous()) / self.hd ** 0.5, dim=-1) @ v
         o = att.to(torch.bfloat16).transpose(0, 1).reshape(S, d)
         x = x + gate_a * lin(o, self.out)
-        m = rms_modulate(x, self.norm_f, scale_f, shift_f)
+        m = rms_modulate(x, self.norm_f, scale_f, shift_f, to_bf16=not w8)
         h = lin(m, self.up, act=True).to(torch.bfloat16)
         return x + gate_f * lin(h, self.down)
 

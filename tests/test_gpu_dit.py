@@ -24,6 +24,25 @@ def test_block_matches_fp32_reference(S, d, heads):
     assert rel <= 2e-2, f"relative error of the update {rel:.3e}"
 
 
+@pytest.mark.parametrize("S,d,heads,group", [(256, 384, 3, 64), (300, 256, 2, 256), (128, 256, 2, 0)])
+def test_w8a8_block_matches_fp32_reference(S, d, heads, group):
+    # The W8A8 route (norms writing the int8 operand, int8 × int8 products) against the fp32 block
+    # whose operands are quantized the same way (per row after the rotation) — the bar of the bf16
+    # route: the fused attention's bf16 probabilities dominate.
+    from siliconed_amd.dit_block import DiTBlock
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=S + group, route="w8a8", group=group)
+    g = torch.Generator(device="cuda:0").manual_seed(2)
+    x = torch.randn((S, d), device="cuda:0", generator=g)
+    temb = torch.randn(d, device="cuda:0", generator=g)
+    y = blk.forward(x, temb)
+    ref = blk.reference(x, temb)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    upd, upd_ref = y - x, ref - x
+    rel = (upd - upd_ref).norm() / upd_ref.norm()
+    assert rel <= 2e-2, f"relative error of the update {rel:.3e}"
+
+
 def test_block_flops():
     from siliconed_amd.dit_block import DiTBlock
     blk = DiTBlock(d=256, heads=2, mlp=4, seed=0)
