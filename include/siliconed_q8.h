@@ -233,6 +233,24 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
                          const float *scale, int scale_layout, const float *bias, int epilogue,
                          void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds);
 
+/* **A product added into the residual stream**: x[m, n] += gate ⊙ (s ⊙ (A·W) + b), x fp32 (leading
+ * dimension ldx) read and written in place, gate fp32 [n] or NULL (1), the sum in fp32 (not rounded
+ * to bf16 first), then x + gate·y with each product and sum rounded on its own. Arguments otherwise
+ * as sq8_linear (no activation); weights packed or [N, K] with K a multiple of 64 (else
+ * SQ8_EUNSUPPORTED). Replaces: the Wo / W_down product and `x += gate · …` of a DiT block
+ * (MossImage.swift:15-19; the residual loop of ElementwiseGPUAnima.swift:47-62), one pass. */
+int sq8_linear_residual(sq8_ctx *ctx,
+                        const void *a, int a_dtype, int64_t lda,
+                        const void *w, int w_dtype, int w_layout, int64_t ldw,
+                        const float *scale, int scale_layout, const float *bias, const float *gate,
+                        float *x, int64_t ldx, int m, int k, int n, double *gpu_seconds);
+
+/* The same on the W8A8 route: x += gate ⊙ (float(Σ codes·q) · (s_x · s_w) + b). */
+int sq8_linear_w8a8_residual(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx,
+                             const void *w, int w_layout, int64_t ldw,
+                             const float *scale, int scale_layout, const float *bias, const float *gate,
+                             float *x, int64_t ldx, int m, int k, int n, double *gpu_seconds);
+
 /* **The W8A8 fused QKV product**: sq8_linear_w8a8 of n = 3·d columns whose outputs [0,d), [d,2d),
  * [2d,3d) go to q, k, v — row-major [m, d] (head_dim 0, leading dimension ldo) or head-major
  * [d/head_dim, m, head_dim]; bias if given, no activation. Replaces: the fused QKV of a block whose

@@ -42,6 +42,10 @@ SIGNATURES = {
                                  ctypes.POINTER(_D)]),
     "sq8_norm_modulate_rotated": (_I, [_P, _P, _I64, _P, _P, _P, ctypes.c_float, _I, _P, _I64, _P, _I64, _I, _I]),
     "sq8_norm_modulate_quantized": (_I, [_P, _P, _I64, _P, _P, _P, ctypes.c_float, _I, _P, _I64, _P, _P, _I64, _I, _I]),
+    "sq8_linear_residual": (_I, [_P, _P, _I, _I64, _P, _I, _I, _I64, _P, _I, _P, _P, _P, _I64, _I, _I, _I,
+                                 ctypes.POINTER(_D)]),
+    "sq8_linear_w8a8_residual": (_I, [_P, _P, _I64, _P, _P, _I, _I64, _P, _I, _P, _P, _P, _I64, _I, _I, _I,
+                                      ctypes.POINTER(_D)]),
     "sq8_packed_bytes": (_I64, [_I, _I, _I]),
     "sq8_pack_weight": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P]),
     "sq8_dequantize": (_I, [_P, _P, _I, _I64, _I64, _P, _I, _I, _I64, _I64, _P]),

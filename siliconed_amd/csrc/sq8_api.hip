@@ -99,6 +99,7 @@ struct Product {
     void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
     int m, k, n;
     int group;  // convrot: the operand rotated by groups of `group` first (0: none)
+    bool residual; const float *gate;  // c (fp32) += gate ⊙ (s ⊙ (A·W) + b), in place
 };
 
 int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
@@ -115,6 +116,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
     if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
+    if (q.residual && (q.c_dtype != SQ8_F32 || is_glu(q.epilogue) || q.k % 64 != 0)) return SQ8_EUNSUPPORTED;
     // The kernels address A and W with 32-bit byte offsets from their bases.
     if ((int64_t)q.m * (q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
         (is_packed(q.w_layout) ? sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue))
@@ -200,8 +202,10 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (q.split > 0) cv16 = cv16 && (q.split % per16) == 0;
     if (q.head_dim > 0) cv16 = cv16 && (q.head_dim % per16) == 0;
     else cv16 = cv16 && (q.ldc % per16) == 0;
-    p.c_vec16 = cv16;
+    p.c_vec16 = cv16 && (!q.gate || aligned(q.gate, 16));
+    p.gate = q.gate;
     p.sb_vec = aligned(p.scale, 16) && (!p.bias || aligned(p.bias, 16)) && (p.glu_half % 4) == 0;
+    const int epi = q.residual ? sq8::EPI_RESIDUAL : q.epilogue;
 
     const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
@@ -234,7 +238,9 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         if (force && strcmp(force, "128") == 0) tile = sq8::WD_128;
         if (force && strcmp(force, "s64") == 0) tile = sq8::WD_SKINNY64;
         if (force && strcmp(force, "s32") == 0) tile = sq8::WD_SKINNY32;
-        e = sq8::launch_wdirect(p, tile, wt, wl, q.epilogue, out, ctx->stream);
+        e = sq8::launch_wdirect(p, tile, wt, wl, epi, out, ctx->stream);
+    } else if (q.residual) {
+        return SQ8_EUNSUPPORTED;  // the residual epilogue runs on the weight-direct kernels only
     } else {
         const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
         const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
@@ -264,6 +270,7 @@ struct W8A8 {
     const float *scale; int scale_layout; const float *bias; int epilogue;
     void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
     int m, k, n;
+    bool residual; const float *gate;  // c (fp32) += gate ⊙ (…), in place
 };
 
 int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
@@ -275,6 +282,7 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     if (is_glu(q.epilogue) && (q.n % 2) != 0) return SQ8_EINVAL;
     if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
     if (q.k >= (1 << 17)) return SQ8_EUNSUPPORTED;  // the int32 sums stay exact below 2^17 terms
+    if (q.residual && (q.c_dtype != SQ8_F32 || is_glu(q.epilogue))) return SQ8_EUNSUPPORTED;
     if (q.a && q.k > sq8::quantize_row_limit()) return SQ8_EUNSUPPORTED;
     const int n_out = is_glu(q.epilogue) ? q.n / 2 : q.n;
     if (gpu_seconds) *gpu_seconds = 0.0;
@@ -347,8 +355,9 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     if (q.split > 0) cv16 = cv16 && (q.split % per16) == 0;
     if (q.head_dim > 0) cv16 = cv16 && (q.head_dim % per16) == 0;
     else cv16 = cv16 && (q.ldc % per16) == 0;
-    p.c_vec16 = cv16;
-    p.c_vec = cv16;
+    p.c_vec16 = cv16 && (!q.gate || aligned(q.gate, 16));
+    p.c_vec = p.c_vec16;
+    p.gate = q.gate;
     p.sb_vec = aligned(q.scale, 16) && (!q.bias || aligned(q.bias, 16)) && (p.glu_half % 4) == 0;
     p.kt = k_pad / 128;
     // The weight: packed as staged, [N, K] read in place when its rows hold whole steps, else
@@ -371,7 +380,8 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
         p.w = static_cast<const uint8_t *>(ctx->wpack);
         p.kt_w = (q.k + 63) / 64;
     }
-    e = sq8::launch_i8gemm(p, wl, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16, ctx->stream);
+    e = sq8::launch_i8gemm(p, wl, q.residual ? sq8::EPI_RESIDUAL : q.epilogue,
+                           q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16, ctx->stream);
     if (e != hipSuccess) return hip_status(e);
     if (gpu_seconds) {
         e = hipEventRecord(ctx->end, ctx->stream);
@@ -553,6 +563,34 @@ int sq8_linear_w8a8(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float 
     q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
     q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
     q.m = m; q.k = k; q.n = n;
+    return run_w8a8(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_residual(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_dtype, int w_layout,
+                        int64_t ldw, const float *scale, int scale_layout, const float *bias, const float *gate, float *x,
+                        int64_t ldx, int m, int k, int n, double *gpu_seconds) {
+    Product q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda;
+    q.w = w; q.w_dtype = w_dtype; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = SQ8_EPI_NONE;
+    q.c[0] = x; q.c_dtype = SQ8_F32; q.ldc = ldx;
+    q.m = m; q.k = k; q.n = n;
+    q.residual = true; q.gate = gate;
+    return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_w8a8_residual(sq8_ctx *ctx, const int8_t *codes, int64_t ldq, const float *sx, const void *w, int w_layout,
+                             int64_t ldw, const float *scale, int scale_layout, const float *bias, const float *gate,
+                             float *x, int64_t ldx, int m, int k, int n, double *gpu_seconds) {
+    W8A8 q;
+    memset(&q, 0, sizeof(q));
+    q.codes = codes; q.ldq = ldq; q.sx = sx;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = SQ8_EPI_NONE;
+    q.c[0] = x; q.c_dtype = SQ8_F32; q.ldc = ldx;
+    q.m = m; q.k = k; q.n = n;
+    q.residual = true; q.gate = gate;
     return run_w8a8(ctx, q, gpu_seconds);
 }
 

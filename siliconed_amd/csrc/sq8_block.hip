@@ -215,6 +215,47 @@ __global__ void __launch_bounds__(256) rms_rows_kernel(uint16_t *__restrict__ t,
     }
 }
 
+// Rows of 128 (the heads of q and k): 16 lanes per row, 8 values (16 bytes) a lane, four rows per
+// wave, sixteen per workgroup, rows looped over the grid. The same arithmetic as rms_rows_kernel (the
+// sum of squares in another order).
+__global__ void __launch_bounds__(256) rms_rows128_kernel(uint16_t *__restrict__ t, int64_t ld, int64_t rows,
+                                                          const float *__restrict__ w, float eps) {
+    const int lane = threadIdx.x & 63, sub = lane & 15;
+    const int64_t slot = (int64_t)(threadIdx.x >> 4);  // 16 rows per workgroup
+    float wv[8];
+    {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(w + 8 * sub);
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(w + 8 * sub + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { wv[e] = a[e]; wv[4 + e] = b[e]; }
+    }
+    for (int64_t base = (int64_t)blockIdx.x * 16; base < rows; base += (int64_t)gridDim.x * 16) {
+        const int64_t row = base + slot;
+        const bool live = row < rows;  // the shuffles below run in every lane: the row's 16 lanes agree
+        u32x4 d = u32x4{0, 0, 0, 0};
+        uint16_t *p = t + row * ld + 8 * sub;
+        if (live) d = *reinterpret_cast<const u32x4 *>(p);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(d[e] << 16);
+            v[2 * e + 1] = __uint_as_float(d[e] & 0xFFFF0000u);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(v[e], v[e]));
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, o, 64));
+        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = round_bf16(__fmul_rn(__fmul_rn(v[2 * e], r), wv[2 * e])) |
+                   round_bf16(__fmul_rn(__fmul_rn(v[2 * e + 1], r), wv[2 * e + 1])) << 16;
+        if (live) *reinterpret_cast<u32x4 *>(p) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 // x += gate ⊙ y, the product rounded then the sum (ElementwiseGPUAnima.swift:47-62); y bf16 or fp32.
 template <bool Y_BF16>
 __global__ void __launch_bounds__(256) gated_residual_kernel(float *__restrict__ x, int64_t ldx, const void *__restrict__ y,
@@ -279,7 +320,11 @@ hipError_t launch_rms_rows(uint16_t *t, int64_t ld, int64_t rows, int cols, cons
     if (rows == 0 || cols == 0) return hipSuccess;
     const dim3 grid((unsigned)((rows + 3) / 4));
     const bool aligned = ((uintptr_t)t & 7) == 0 && ld % 4 == 0;
-    if (!aligned) hipLaunchKernelGGL(rms_rows_kernel<0>, grid, dim3(256), 0, stream, t, ld, rows, cols, w, eps);
+    if (cols == 128 && ((uintptr_t)t & 15) == 0 && ld % 8 == 0 && ((uintptr_t)w & 15) == 0) {
+        const int64_t want = (rows + 15) / 16;
+        hipLaunchKernelGGL(rms_rows128_kernel, dim3((unsigned)(want < 65535 ? want : 65535)), dim3(256), 0, stream, t, ld,
+                           rows, w, eps);
+    } else if (!aligned) hipLaunchKernelGGL(rms_rows_kernel<0>, grid, dim3(256), 0, stream, t, ld, rows, cols, w, eps);
     else if (cols == 128) hipLaunchKernelGGL(rms_rows_kernel<2>, grid, dim3(256), 0, stream, t, ld, rows, cols, w, eps);
     else if (cols == 256) hipLaunchKernelGGL(rms_rows_kernel<4>, grid, dim3(256), 0, stream, t, ld, rows, cols, w, eps);
     else if (cols == 64) hipLaunchKernelGGL(rms_rows_kernel<1>, grid, dim3(256), 0, stream, t, ld, rows, cols, w, eps);

@@ -27,7 +27,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 enum WType { W_INT8 = 0, W_FP8 = 1 };
 enum WLayout { W_KN = 0, W_NK = 1, W_PACKED = 2 };
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_SILU_GLU = 2, EPI_SITU_GLU = 3 };
+// EPI_RESIDUAL (fp32 output only): C += gate ⊙ (s·acc + b), C the caller's residual stream read and
+// written in place (the product rounded, then the sum: the gated residual pass's arithmetic).
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_SILU_GLU = 2, EPI_SITU_GLU = 3, EPI_RESIDUAL = 4 };
 enum OutT { OUT_BF16 = 0, OUT_F32 = 1 };
 
 // Two fp32 values that are exactly bf16 values (every int8 and every e4m3 code is) packed into one

@@ -29,6 +29,7 @@ struct GemmArgs {
     int sb_vec;             // 16-byte loads of 4 scales / biases allowed (aligned bases, GLU half % 4 == 0)
     int kt;                 // K steps of 64 (the packed layout's K extent); W8A8: K steps of 128
     int tiles_m, tiles_n;   // set by the launcher
+    const float *gate;      // EPI_RESIDUAL: per-column gate fp32 [N], or null (1)
     const float *sx;        // W8A8: the activation's row scales fp32 [M] (`a` then holds int8 codes)
     int kt_w;               // W8A8: K steps of 64 of the packed weight
 };

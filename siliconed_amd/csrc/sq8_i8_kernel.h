@@ -255,6 +255,7 @@ hipError_t dispatch_i8(const GemmArgs &p, int epi, int out, hipStream_t stream) 
     SQ8_CASE(EPI_SILU_GLU, OUT_F32)
     SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
     SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    SQ8_CASE(EPI_RESIDUAL, OUT_F32)
 #undef SQ8_CASE
     return hipErrorInvalidValue;
 }

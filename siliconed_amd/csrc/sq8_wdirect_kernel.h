@@ -188,7 +188,24 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
         const int m = m_first + row;
         const int col = col0 + chunk * PER;
         if (m < p.M && col < n_out) {
-            if (col + PER <= n_out && p.c_vec16) {
+            if constexpr (EPI == EPI_RESIDUAL) {
+                // x = x + gate·y, y the fp32 sum scaled and biased (OUT_F32: 4 values a chunk).
+                static_assert(OUT == OUT_F32, "the residual stream is fp32");
+                float *xr = reinterpret_cast<float *>(p.c[0]) + (int64_t)m * p.ldc + col;
+                if (col + PER <= n_out && p.c_vec16) {
+                    const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr);
+                    const f32x4 gv = p.gate ? *reinterpret_cast<const f32x4 *>(p.gate + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = __fadd_rn(xv[e], __fmul_rn(gv[e], __uint_as_float(v[e])));
+                    *reinterpret_cast<f32x4 *>(xr) = o;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < PER; ++e)
+                        if (col + e < n_out)
+                            xr[e] = __fadd_rn(xr[e], __fmul_rn(p.gate ? p.gate[col + e] : 1.0f, __uint_as_float(v[e])));
+                }
+            } else if (col + PER <= n_out && p.c_vec16) {
                 int which;
                 const int64_t off = out_index(p, m, col, which);
                 *reinterpret_cast<u32x4 *>(kern::out_base(p, which) + off * ESZ) = v;
@@ -489,6 +506,7 @@ hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) 
     SQ8_CASE(EPI_SILU_GLU, OUT_F32)
     SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
     SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    SQ8_CASE(EPI_RESIDUAL, OUT_F32)
 #undef SQ8_CASE
     return hipErrorInvalidValue;
 }

@@ -111,18 +111,19 @@ class DiTBlock:
         ctx.rms_rows(k.view(S * self.heads, self.hd), self.norm_k, EPS)
         heads = lambda t: t.view(S, self.heads, self.hd).transpose(0, 1)
         o = attention(heads(q), heads(k), heads(v)).transpose(0, 1).reshape(S, d)
-        ctx.gated_residual(x, self._product8(ctx.quantize_rows(o, g), self.out), gate_a)
+        o8 = ctx.quantize_rows(o, g)
+        ctx.product_w8a8_residual(x, o8[0], o8[1], self.out["packed"], self.out["s"], bias=self.out["b"], gate=gate_a)
         m8 = ctx.norm_modulate_quantized(x, self.norm_f, scale_f, shift_f, EPS, g)
-        h = self._product8(m8, self.up, epilogue="gelu_tanh")
-        ctx.gated_residual(x, self._product8(ctx.quantize_rows(h, g), self.down), gate_f)
+        h8 = ctx.quantize_rows(self._product8(m8, self.up, epilogue="gelu_tanh"), g)
+        ctx.product_w8a8_residual(x, h8[0], h8[1], self.down["packed"], self.down["s"], bias=self.down["b"], gate=gate_f)
         return x
 
     def forward_(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
         """The block on the residual stream x (fp32 [S, d], contiguous), updated in place as the
         reference's stream buffer is; temb [d]. Every pass but the attention is this library's: the
-        modulation, the fused QKV (rows [S, heads·hd]: q, k, v are [heads, S, hd] views), Wo, W_up with
-        GELU fused and W_down products; the modulated norms, the per-head norms of q and k and the
-        gated residual updates."""
+        modulation, the fused QKV (rows [S, heads·hd]: q, k, v are [heads, S, hd] views), Wo and W_down
+        with the gated residual update fused (x += gate ⊙ product, the product in fp32), W_up with GELU
+        fused; the modulated norms and the per-head norms of q and k."""
         if self.route == "w8a8":
             return self._forward_w8a8(x, temb)
         S, d = x.shape
@@ -135,10 +136,10 @@ class DiTBlock:
         ctx.rms_rows(k.view(S * self.heads, self.hd), self.norm_k, EPS)
         heads = lambda t: t.view(S, self.heads, self.hd).transpose(0, 1)                        # [heads, S, hd]
         o = attention(heads(q), heads(k), heads(v)).transpose(0, 1).reshape(S, d)
-        ctx.gated_residual(x, self._product(o, self.out), gate_a)
+        ctx.product_residual(x, o, self.out["packed"], self.out["s"], bias=self.out["b"], gate=gate_a)
         m = ctx.norm_modulate(x, self.norm_f, scale_f, shift_f, EPS)
         h = self._product(m, self.up, epilogue="gelu_tanh")
-        ctx.gated_residual(x, self._product(h, self.down), gate_f)
+        ctx.product_residual(x, h, self.down["packed"], self.down["s"], bias=self.down["b"], gate=gate_f)
         return x
 
     def forward(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:

@@ -476,6 +476,48 @@ class TensorGEMM:
         abi.check(st, "sq8_linear_w8a8_qkv")
         return out
 
+    def product_residual(self, x: torch.Tensor, a: torch.Tensor, w, scale: torch.Tensor, *, layout: str = "nk",
+                         bias: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None,
+                         fp8: Optional[bool] = None) -> torch.Tensor:
+        """x += gate ⊙ (s ⊙ (a · Wᵀ) + b) in place (x fp32 [m, n], the residual stream), one pass."""
+        m, k = a.shape
+        if isinstance(w, PackedWeight):
+            lay, wd, n, ldw, wptr = w.layout, w.w_dtype, w.n, w.k, _dev(w.data, "w")
+        else:
+            lay, wd = _LAYOUTS[layout], _wdtype(w, fp8)
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            ldw, wptr = _row_major(w, "w"), _dev(w, "w")
+        if x.dtype != torch.float32 or tuple(x.shape) != (m, n):
+            raise ValueError("x must be the fp32 residual stream [m, n]")
+        st = abi.load().sq8_linear_residual(
+            self._h, _dev(a, "a"), _adtype(a), _row_major(a, "a"), wptr, wd, lay, ldw,
+            _dev(scale, "scale"), abi.SCALE_COLUMNS if scale.numel() != 1 else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"), None if gate is None else _dev(gate, "gate"),
+            _dev(x, "x"), _row_major(x, "x"), m, k, n, None)
+        abi.check(st, "sq8_linear_residual")
+        return x
+
+    def product_w8a8_residual(self, x: torch.Tensor, codes: torch.Tensor, sx: torch.Tensor, w, scale: torch.Tensor, *,
+                              layout: str = "nk", bias: Optional[torch.Tensor] = None,
+                              gate: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x += gate ⊙ (float(codes · qᵀ) · (s_x · s_w) + b) in place, one pass."""
+        m, k = codes.shape
+        if isinstance(w, PackedWeight):
+            lay, n, ldw, wptr = w.layout, w.n, w.k, _dev(w.data, "w")
+        else:
+            lay = _LAYOUTS[layout]
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            ldw, wptr = _row_major(w, "w"), _dev(w, "w")
+        if x.dtype != torch.float32 or tuple(x.shape) != (m, n):
+            raise ValueError("x must be the fp32 residual stream [m, n]")
+        st = abi.load().sq8_linear_w8a8_residual(
+            self._h, _dev(codes, "codes"), _row_major(codes, "codes"), _dev(sx, "sx"), wptr, lay, ldw,
+            _dev(scale, "scale"), abi.SCALE_COLUMNS if scale.numel() != 1 else abi.SCALE_TENSOR,
+            None if bias is None else _dev(bias, "bias"), None if gate is None else _dev(gate, "gate"),
+            _dev(x, "x"), _row_major(x, "x"), m, k, n, None)
+        abi.check(st, "sq8_linear_w8a8_residual")
+        return x
+
     def rms_rows(self, t: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
         """In place: each row of the bf16 tensor t (last dimension ≤ 256, rows contiguous) →
         bf16((t·r)·w) — the per-head RMSNorm of q and k."""

@@ -430,3 +430,24 @@ def test_epilogue_rounds_scale_then_bias(gemm, orc, m, layout):
     y = gemm.product(x, w, dev(s), layout="nk" if layout == "nk" else "kn", bias=dev(b), out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy(), want)
+
+
+# ---- the gated residual fused into the product (MossImage.swift:15-19, ElementwiseGPUAnima.swift:47-62) ----
+
+@pytest.mark.parametrize("m,layout,gated", [(300, "packed", True), (4096, "packed", False), (40, "nk", True), (1, "packed", True)])
+def test_residual_product_is_product_then_residual(gemm, orc, m, layout, gated):
+    # x + gate·(s·acc + b) in one pass equals the fp32 product then sq8_gated_residual on it, bit for bit.
+    k, n = 1024, 768
+    x_, q, s, b = problem(orc, m, k, n, False, m + 7)
+    stream = orc.normal_f32(m + 9, (m, n), 0.0, 1.0)
+    gate = dev(orc.normal_f32(m + 10, (n,), 0.0, 0.5)) if gated else None
+    w = weight_tensor(q, False, "nk")
+    if layout == "packed":
+        w = gemm.pack(w, layout="nk")
+    y = gemm.product(bf16_dev(x_), w, dev(s), layout="nk", bias=dev(b), out_dtype=torch.float32)
+    expect = dev(stream)
+    gemm.gated_residual(expect, y, gate)
+    got = dev(stream)
+    gemm.product_residual(got, bf16_dev(x_), w, dev(s), layout="nk", bias=dev(b), gate=gate)
+    torch.cuda.synchronize()
+    assert bitwise_equal(got.cpu().numpy(), expect.cpu().numpy()) == 0

@@ -273,3 +273,21 @@ def test_w8a8_qkv_is_the_split_product(gemm, orc, head_dim):
         if head_dim:
             part = part.transpose(1, 0, 2).reshape(m, d)
         assert np.array_equal(part, full[:, i * d:(i + 1) * d]), i
+
+
+def test_w8a8_residual_product_is_product_then_residual(gemm, orc):
+    m, k, n = 300, 1024, 768
+    x = inputs(orc, m, k, 71)
+    q = orc.uniform_i8(72, (n, k))
+    sw = orc.uniform_f32(73, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(74, (n,), 0.0, 0.02)
+    stream = orc.normal_f32(75, (m, n))
+    gate = dev(orc.normal_f32(76, (n,), 0.0, 0.5))
+    codes, sx = orc.quantize_rows(x, 256)
+    w = gemm.pack(dev(q).view(torch.int8), layout="nk")
+    y = dev(orc.w8a8_product(codes, sx, q, False, sw) + b[None, :])
+    expect = dev(stream)
+    gemm.gated_residual(expect, y, gate)
+    got = dev(stream)
+    gemm.product_w8a8_residual(got, dev(codes), dev(sx), w, dev(sw), bias=dev(b), gate=gate)
+    assert bitwise_equal(host(got), host(expect)) == 0
