@@ -62,7 +62,7 @@ enum sq8_wlayout {
 enum sq8_scale_layout {
     SQ8_SCALE_TENSOR = 0,  /* one scale: `perColumn` false (TensorGEMM.swift:264, :353) */
     SQ8_SCALE_COLUMNS = 1, /* one per output channel: `perColumn` true */
-    SQ8_SCALE_BLOCKS = 2,  /* [K/b, N] (dequantize only) */
+    SQ8_SCALE_BLOCKS = 2,  /* [K/b, N] (sq8_dequantize; the product: sq8_linear_blocks) */
     SQ8_SCALE_ROWS = 3,    /* one per row of [N, K] (dequantize only) */
 };
 
@@ -301,6 +301,39 @@ int sq8_rms_rows(sq8_ctx *ctx, uint16_t *t, int64_t ld, int64_t rows, int cols, 
  * residual loop of `residual_modulate` (ElementwiseGPUAnima.swift:47-62). */
 int sq8_gated_residual(sq8_ctx *ctx, float *x, int64_t ldx, const void *y, int y_dtype, int64_t ldy,
                        const float *gate, int64_t rows, int cols);
+
+/* ---- codes with a scale per block of rows and column: GGUF Q8_0 (w = q · d, one fp16 d per 32
+ * consecutive K of an output; Sources/Siliconed/Forge/GGUF.swift, `deinterleaveQ8_0`) ---- */
+
+/* **The product on block scales**: C[m, n_out] = act(A · W + b), W[k, c] = q[k, c] · s[k / block, c],
+ * int8 codes q, `block` a multiple of 32 dividing k (Q8_0: 32), k a multiple of 64. Codes in
+ * `w_layout` SQ8_KN ([k, n], scales [k/block, n] row-major — the map's `[K/b, N]`) or SQ8_NK
+ * ([n, k], scales [n, k/block] — GGUF's rows of blocks), scales of `scale_dtype` SQ8_F32, SQ8_BF16
+ * or SQ8_F16 (widened exactly); or SQ8_PACKED(_GLU): `w` written by sq8_pack_blocks, which holds the
+ * scales (`scale`, `scale_dtype`, `ldw` ignored). Each block's fp32 partial sum of exact bf16 × code
+ * products is scaled once complete (the reference widens q·s first; the two agree in exact
+ * arithmetic). A, bias, epilogues, C, `gpu_seconds` as sq8_linear. Replaces: TensorGEMM.linear(…
+ * block: B …) (TensorGEMM.swift:264-290) and its `linear_q8` encoder (TensorGEMM.swift:137-171,
+ * :307-318), with its rounded-activation route (TensorGEMMBF16.swift, `roundsBlocks`). */
+int sq8_linear_blocks(sq8_ctx *ctx,
+                      const void *a, int a_dtype, int64_t lda,
+                      const void *w, int w_layout, int64_t ldw,
+                      const void *scale, int scale_dtype, int block,
+                      const float *bias, int epilogue,
+                      void *c, int c_dtype, int64_t ldc,
+                      int m, int k, int n, double *gpu_seconds);
+
+/* Bytes of sq8_pack_blocks' layout (codes, then fp32 scales per step and column), or −1. Replaces:
+ * the reserve plan's size of a staged Q8_0 weight (WeightProducts.int8Plan, WeightProducts.swift:535-600). */
+int64_t sq8_packed_blocks_bytes(int k, int n, int glu);
+
+/* **Staging a block-scaled weight**: codes (`w_layout` SQ8_KN or SQ8_NK, `ldw`) and their scales (as
+ * sq8_linear_blocks reads them) rewritten into the packed Q8 layout in `out` (16-byte aligned
+ * device memory of sq8_packed_blocks_bytes bytes). `glu` pairs the halves of a gate-up weight.
+ * Once per weight; queued on the context's stream. Replaces: Artifact.stageInt8's copy of q and
+ * its block scales (Artifact.swift:755-774) for the Q8_0 route. */
+int sq8_pack_blocks(sq8_ctx *ctx, const void *w, int w_layout, int64_t ldw, const void *scale, int scale_dtype,
+                    int block, int k, int n, int glu, void *out);
 
 /* Waits for everything queued on the context's stream. Replaces: waitUntilCompleted /
  * GPUStream.drain (GPUStream.swift). */

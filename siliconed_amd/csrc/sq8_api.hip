@@ -394,6 +394,110 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     return SQ8_OK;
 }
 
+// ---- codes with a scale per block of rows and column (GGUF Q8_0) ----------------------------------
+
+struct Blocks {
+    const void *a; int a_dtype; int64_t lda;
+    const void *w; int w_layout; int64_t ldw;
+    const void *scale; int scale_dtype; int block;
+    const float *bias; int epilogue;
+    void *c; int c_dtype; int64_t ldc;
+    int m, k, n;
+};
+
+bool scale_dtype_ok(int t) { return t == SQ8_F32 || t == SQ8_BF16 || t == SQ8_F16; }
+
+int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
+    if (!ctx) return SQ8_EINVAL;
+    if (q.a_dtype != SQ8_BF16 && q.a_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    if (q.c_dtype != SQ8_BF16 && q.c_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    if (q.w_layout < SQ8_KN || q.w_layout > SQ8_PACKED_GLU) return SQ8_EINVAL;
+    if (q.epilogue < SQ8_EPI_NONE || q.epilogue > SQ8_EPI_SITU_GLU) return SQ8_EINVAL;
+    if (is_packed(q.w_layout) && (q.w_layout == SQ8_PACKED_GLU) != is_glu(q.epilogue)) return SQ8_EINVAL;
+    if (q.m < 0 || q.k < 0 || q.n < 0) return SQ8_EINVAL;
+    if (is_glu(q.epilogue) && (q.n % 2) != 0) return SQ8_EINVAL;
+    const bool packed = is_packed(q.w_layout);
+    if (!packed && !scale_dtype_ok(q.scale_dtype)) return SQ8_EINVAL;
+    if (q.block <= 0) return SQ8_EINVAL;
+    const int n_out = is_glu(q.epilogue) ? q.n / 2 : q.n;
+    if (gpu_seconds) *gpu_seconds = 0.0;
+    if (q.m == 0 || n_out == 0) return SQ8_OK;
+    if (!q.a || !q.w || !q.c || (!packed && !q.scale)) return SQ8_EINVAL;
+    if (q.lda < q.k || q.ldc < n_out) return SQ8_EINVAL;
+    if (!packed && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
+    // Blocks of whole MFMA sub-steps, whole activation tiles, 32-bit offsets into A and the packed codes.
+    if (q.block % 32 != 0 || q.k % q.block != 0 || q.k % 64 != 0) return SQ8_EUNSUPPORTED;
+    if ((int64_t)q.m * (q.a_dtype == SQ8_BF16 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
+        sq8::packed_blocks_bytes(q.k, q.n, is_glu(q.epilogue)) > (int64_t)UINT32_MAX)
+        return SQ8_EUNSUPPORTED;
+    if (packed && !aligned(q.w, 16)) return SQ8_EINVAL;
+
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    sq8::GemmArgs p;
+    memset(&p, 0, sizeof(p));
+    p.a = static_cast<const uint16_t *>(q.a);
+    p.lda = q.lda;
+    if (gpu_seconds) {
+        hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    if (q.a_dtype == SQ8_F32) {
+        // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
+        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
+        if (st != SQ8_OK) return st;
+        const float *x = static_cast<const float *>(q.a);
+        uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
+        for (int r = 0; r < (q.lda == q.k ? 1 : q.m); ++r) {
+            const int64_t count = q.lda == q.k ? (int64_t)q.m * q.k : q.k;
+            hipError_t e = sq8::launch_round_bf16(x + (int64_t)r * q.lda, y + (int64_t)r * q.k, count, ctx->stream);
+            if (e != hipSuccess) return hip_status(e);
+        }
+        p.a = y;
+        p.lda = q.k;
+    }
+    if (!aligned(p.a, 16) || (p.lda % 8) != 0) return SQ8_EUNSUPPORTED;
+    p.w = static_cast<const uint8_t *>(q.w);
+    if (!packed) {
+        // The codes and their scales packed per product into the context's buffer (the reference
+        // reads the map's [K, N] codes and [K/B, N] scales in place, TensorGEMM.swift:307-318).
+        const int64_t bytes = sq8::packed_blocks_bytes(q.k, q.n, is_glu(q.epilogue));
+        int st = reserve_buffer(ctx, &ctx->wpack, &ctx->wpack_bytes, (size_t)bytes);
+        if (st != SQ8_OK) return st;
+        hipError_t e = sq8::launch_pack_blocks(p.w, q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK, q.ldw, q.scale,
+                                               q.scale_dtype, q.block, q.k, q.n, is_glu(q.epilogue),
+                                               static_cast<uint8_t *>(ctx->wpack), ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        p.w = static_cast<const uint8_t *>(ctx->wpack);
+    }
+    p.bias = q.bias;
+    p.c[0] = q.c;
+    p.ldc = q.ldc;
+    p.M = q.m;
+    p.N = q.n;
+    p.K = q.k;
+    p.kt = q.k / 64;
+    p.glu_half = is_glu(q.epilogue) ? q.n / 2 : 0;
+    const size_t esz = q.c_dtype == SQ8_F32 ? 4 : 2;
+    p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
+    int tile = sq8::Q8_64x256;
+    const char *force = getenv("SQ8_Q8_TILE");  // measurement knob: "512"
+    if (force && strcmp(force, "512") == 0) tile = sq8::Q8_64x512;
+    hipError_t e = sq8::launch_q8(p, tile, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16,
+                                  ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+    if (gpu_seconds) {
+        e = hipEventRecord(ctx->end, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->end);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->begin, ctx->end);
+        if (e != hipSuccess) return hip_status(e);
+        *gpu_seconds = (double)ms * 1e-3;
+    }
+    return SQ8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -738,6 +842,43 @@ int sq8_synchronize(sq8_ctx *ctx) {
     DeviceScope scope(ctx->device);
     if (scope.error != hipSuccess) return hip_status(scope.error);
     return hip_status(hipStreamSynchronize(ctx->stream));
+}
+
+
+int64_t sq8_packed_blocks_bytes(int k, int n, int glu) {
+    if (k < 0 || n < 0 || (glu && (n % 2) != 0)) return -1;
+    return sq8::packed_blocks_bytes(k, n, glu != 0);
+}
+
+int sq8_pack_blocks(sq8_ctx *ctx, const void *w, int w_layout, int64_t ldw, const void *scale, int scale_dtype,
+                    int block, int k, int n, int glu, void *out) {
+    if (!ctx || k < 0 || n < 0 || (glu && (n % 2) != 0) || block <= 0) return SQ8_EINVAL;
+    if (w_layout != SQ8_KN && w_layout != SQ8_NK) return SQ8_EINVAL;
+    if (!scale_dtype_ok(scale_dtype)) return SQ8_EINVAL;
+    if (ldw < (w_layout == SQ8_KN ? n : k)) return SQ8_EINVAL;
+    if (block % 32 != 0 || k % block != 0) return SQ8_EUNSUPPORTED;
+    if (k == 0 || n == 0) return SQ8_OK;
+    if (!w || !scale || !out) return SQ8_EINVAL;
+    if (!aligned(out, 16)) return SQ8_EINVAL;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    return hip_status(sq8::launch_pack_blocks(static_cast<const uint8_t *>(w), w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK,
+                                              ldw, scale, scale_dtype, block, k, n, glu != 0,
+                                              static_cast<uint8_t *>(out), ctx->stream));
+}
+
+int sq8_linear_blocks(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_layout, int64_t ldw,
+                      const void *scale, int scale_dtype, int block, const float *bias, int epilogue, void *c,
+                      int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    Blocks q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_dtype = scale_dtype; q.block = block;
+    q.bias = bias; q.epilogue = epilogue;
+    q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    return run_blocks(ctx, q, gpu_seconds);
 }
 
 }  // extern "C"

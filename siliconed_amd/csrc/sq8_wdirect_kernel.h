@@ -142,41 +142,15 @@ __device__ __forceinline__ void load_col_params(const GemmArgs &p, ColParams &cp
     }
 }
 
-// Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
-// `x` (and `u`, with `cu`), written to the wave's LDS region as rows of 32 values, then stored as
-// 16-byte row segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
+// The second half of an epilogue: a wave's LDS region of 32 rows × 32 finished values (row pitch
+// 32·size + 16) read back as 16-byte row segments and stored (the residual epilogue adds them to
+// the fp32 stream). Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
 template <int EPI, int OUT>
-__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
-                                            const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
-                                            uint8_t *region, int lane) {
-    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
+__device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_first, int n_out, const uint8_t *region,
+                                             int lane) {
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
-    constexpr int PITCH = 32 * ESZ + 16;  // row bytes + 16: keeps 16-byte alignment, spreads banks
-    const int h = lane >> 5, r = lane & 31;
-    static_for<0, 4>([&](auto gc) {
-        constexpr int g = decltype(gc)::value;
-        const int c = 8 * g + 4 * h;  // first of this lane's 4 columns in the block
-        float y[4];
-        static_for<0, 4>([&](auto ec) {
-            constexpr int e = decltype(ec)::value;
-            float v = __fmul_rn(x[4 * g + e], cx.s[g][e]);
-            if (has_bias) v = __fadd_rn(v, cx.b[g][e]);
-            if constexpr (EPI == EPI_GELU) {
-                v = gelu_tanh(v);
-            } else if constexpr (GLU) {
-                float w = __fmul_rn(u[4 * g + e], cu.s[g][e]);
-                if (has_bias) w = __fadd_rn(w, cu.b[g][e]);
-                v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
-            }
-            y[e] = v;
-        });
-        uint8_t *dst = region + r * PITCH + c * ESZ;
-        if constexpr (OUT == OUT_BF16)
-            *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
-        else
-            *reinterpret_cast<f32x4 *>(dst) = f32x4{y[0], y[1], y[2], y[3]};
-    });
-    // Read back as 16-byte row segments: CPR chunks per row, 64/CPR rows per pass. LDS operations
+    constexpr int PITCH = 32 * ESZ + 16;
+    // 16-byte row segments: CPR chunks per row, 64/CPR rows per pass. LDS operations
     // of one wave complete in order, so the wave reads back what it just wrote.
     constexpr int CPR = 32 * ESZ / 16;
     constexpr int ROWS = 64 / CPR;
@@ -225,6 +199,44 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
             }
         }
     });
+}
+
+
+// Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
+// `x` (and `u`, with `cu`), written to the wave's LDS region as rows of 32 values, then stored as
+// 16-byte row segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
+                                            const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
+                                            uint8_t *region, int lane) {
+    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
+    constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
+    constexpr int PITCH = 32 * ESZ + 16;  // row bytes + 16: keeps 16-byte alignment, spreads banks
+    const int h = lane >> 5, r = lane & 31;
+    static_for<0, 4>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        const int c = 8 * g + 4 * h;  // first of this lane's 4 columns in the block
+        float y[4];
+        static_for<0, 4>([&](auto ec) {
+            constexpr int e = decltype(ec)::value;
+            float v = __fmul_rn(x[4 * g + e], cx.s[g][e]);
+            if (has_bias) v = __fadd_rn(v, cx.b[g][e]);
+            if constexpr (EPI == EPI_GELU) {
+                v = gelu_tanh(v);
+            } else if constexpr (GLU) {
+                float w = __fmul_rn(u[4 * g + e], cu.s[g][e]);
+                if (has_bias) w = __fadd_rn(w, cu.b[g][e]);
+                v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
+            }
+            y[e] = v;
+        });
+        uint8_t *dst = region + r * PITCH + c * ESZ;
+        if constexpr (OUT == OUT_BF16)
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
+        else
+            *reinterpret_cast<f32x4 *>(dst) = f32x4{y[0], y[1], y[2], y[3]};
+    });
+    flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
 }
 
 template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT>

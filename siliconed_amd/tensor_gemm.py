@@ -39,6 +39,21 @@ class PackedWeight:
         return abi.PACKED_GLU if self.glu else abi.PACKED
 
 
+class PackedBlocks:
+    """A block-scaled weight (GGUF Q8_0) staged by sq8_pack_blocks: `k` × `n` int8 codes and their
+    scales per `block` rows, paired for a GLU epilogue when `glu`."""
+
+    def __init__(self, data: torch.Tensor, k: int, n: int, glu: bool, block: int):
+        self.data, self.k, self.n, self.glu, self.block = data, k, n, glu, block
+
+    @property
+    def layout(self) -> int:
+        return abi.PACKED_GLU if self.glu else abi.PACKED
+
+
+_SCALE_DTYPES = {torch.float32: abi.F32, torch.bfloat16: abi.BF16, torch.float16: abi.F16}
+
+
 def _epilogue(name) -> int:
     if name not in _EPILOGUES:
         raise ValueError(f"unknown epilogue {name!r}")
@@ -151,11 +166,33 @@ class TensorGEMM:
         `prequantized` = (codes, scales) of `a` already quantized skips that pass.
 
         Routes this library does not take raise `abi.Unsupported` before any work, as the
-        reference's `nil` pipelines send the caller back to the widened route: Q8_0 `block`
-        scales, an fp32 activation not rounded.
+        reference's `nil` pipelines send the caller back to the widened route: an fp32 activation
+        not rounded, block scales with a rotation or a W8A8 quantization.
+
+        `block` = B: scales per block of B rows of K and column (GGUF Q8_0, fp32 `[k / B, n]` at
+        `scales_offset`; `per_column` ignored), the product of sq8_linear_blocks.
         """
         if block is not None:
-            raise abi.Unsupported(abi.EUNSUPPORTED, "Q8_0 block scales")
+            if rotation is not None or quantizing is not None or prequantized is not None or fp8:
+                raise abi.Unsupported(abi.EUNSUPPORTED, "block scales take int8 codes, no rotation, bf16 operands")
+            if a.dtype == torch.float32 and not rounding:
+                raise abi.Unsupported(abi.EUNSUPPORTED, "fp32 activations without bf16 rounding")
+            lay = _LAYOUTS[layout]
+            epi = _epilogue(epilogue)
+            n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
+            if a.numel() < m * k or c.numel() < m * n_out or int8.numel() < weight_offset + k * n:
+                raise ValueError("a, c or the weight buffer smaller than m × k, m × n, k × n")
+            if scales.dtype != torch.float32 or scales_offset % 4 or \
+                    scales.numel() * 4 < scales_offset + 4 * (k // max(int(block), 1)) * n:
+                raise ValueError("scales must be fp32, [k / block, n] after the offset (a multiple of 4 bytes)")
+            secs = ctypes.c_double(0.0)
+            st = abi.load().sq8_linear_blocks(self._h, _dev(a, "a"), _adtype(a), k, _dev(int8, "int8") + weight_offset,
+                                              lay, n if lay == abi.KN else k, _dev(scales, "scales") + scales_offset,
+                                              abi.F32, int(block), None if bias is None else _dev(bias, "bias"), epi,
+                                              _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                              None if settled else ctypes.byref(secs))
+            abi.check(st, "sq8_linear_blocks")
+            return 0.0 if settled else secs.value
         group = 0 if rotation is None else int(rotation[0] if isinstance(rotation, (tuple, list)) else rotation)
         if quantizing is not None or prequantized is not None:
             if fp8:
@@ -302,6 +339,66 @@ class TensorGEMM:
         st = abi.load().sq8_pack_weight(self._h, _dev(w, "w"), lay, _row_major(w, "w"), k, n, int(glu), out.data_ptr())
         abi.check(st, "sq8_pack_weight")
         return PackedWeight(out, k, n, glu, wd)
+
+    def pack_blocks(self, w: torch.Tensor, scale: torch.Tensor, block: int, *, layout: str = "nk",
+                    glu: bool = False) -> PackedBlocks:
+        """Stages block-scaled int8 codes W ([n, k] "nk" with scales [n, k/block]; [k, n] "kn" with
+        scales [k/block, n]; scales fp32, bf16 or fp16) into the packed Q8 layout, once."""
+        lay = _LAYOUTS[layout]
+        if w.dtype != torch.int8 or w.dim() != 2:
+            raise ValueError("block scales take int8 codes, 2-D")
+        n, k = (w.shape[0], w.shape[1]) if lay == abi.NK else (w.shape[1], w.shape[0])
+        if block <= 0 or k % block:
+            raise ValueError(f"k = {k} is not a multiple of the block {block}")
+        want = (n, k // block) if lay == abi.NK else (k // block, n)
+        if scale.dtype not in _SCALE_DTYPES or tuple(scale.shape) != want or not scale.is_contiguous():
+            raise ValueError(f"scale must be contiguous fp32/bf16/fp16 {want}")
+        size = abi.load().sq8_packed_blocks_bytes(k, n, int(glu))
+        if size < 0:
+            raise ValueError("a GLU weight has an even number of columns")
+        out = torch.empty(max(size, 1), dtype=torch.uint8, device=w.device)
+        st = abi.load().sq8_pack_blocks(self._h, _dev(w, "w"), lay, _row_major(w, "w"), _dev(scale, "scale"),
+                                        _SCALE_DTYPES[scale.dtype], int(block), k, n, int(glu), out.data_ptr())
+        abi.check(st, "sq8_pack_blocks")
+        return PackedBlocks(out, k, n, glu, int(block))
+
+    def product_blocks(self, x: torch.Tensor, w, scale: Optional[torch.Tensor] = None, block: int = 32, *,
+                       layout: str = "nk", bias: Optional[torch.Tensor] = None, epilogue=None,
+                       out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+                       timed: bool = False):
+        """y = act(x · Wᵀ + b), W[n, k] = q · s[block of k, n] (GGUF Q8_0: block 32): x [m, k] bf16
+        (or fp32, rounded); W int8 codes [n, k] ("nk", scales [n, k/block]) or [k, n] ("kn",
+        scales [k/block, n]), or a PackedBlocks (scale and block from it)."""
+        epi = _epilogue(epilogue)
+        m, k = x.shape
+        if isinstance(w, PackedBlocks):
+            if w.k != k:
+                raise ValueError(f"x [{m}, {k}] and the packed weight disagree on K ({w.k})")
+            if w.glu != (epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU)):
+                raise ValueError("a weight packed for a GLU epilogue serves GLU epilogues only, and only those")
+            lay, n, ldw, wptr, sptr, sdt, block = w.layout, w.n, w.k, _dev(w.data, "w"), None, abi.F32, w.block
+        else:
+            lay = _LAYOUTS[layout]
+            if w.dtype != torch.int8 or w.dim() != 2:
+                raise ValueError("block scales take int8 codes, 2-D")
+            n = w.shape[0] if lay == abi.NK else w.shape[1]
+            if (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
+                raise ValueError(f"x [{m}, {k}] and w {tuple(w.shape)} ({layout}) disagree on K")
+            want = (n, k // block) if lay == abi.NK else (k // block, n)
+            if scale is None or scale.dtype not in _SCALE_DTYPES or tuple(scale.shape) != want or \
+                    not scale.is_contiguous():
+                raise ValueError(f"scale must be contiguous fp32/bf16/fp16 {want}")
+            ldw, wptr, sptr, sdt = _row_major(w, "w"), _dev(w, "w"), _dev(scale, "scale"), _SCALE_DTYPES[scale.dtype]
+        n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
+        if out is None:
+            out = torch.empty((m, n_out), dtype=out_dtype, device=x.device)
+        secs = ctypes.c_double(0.0)
+        st = abi.load().sq8_linear_blocks(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"), wptr, lay, ldw, sptr,
+                                          sdt, int(block), None if bias is None else _dev(bias, "bias"), epi,
+                                          _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+                                          ctypes.byref(secs) if timed else None)
+        abi.check(st, "sq8_linear_blocks")
+        return (out, secs.value) if timed else out
 
     # ---- tensor-level operations ---------------------------------------------------------------
 

@@ -45,11 +45,12 @@ def weight_tensor(q: np.ndarray, fp8: bool, layout: str) -> torch.Tensor:
     return t.view(torch.float8_e4m3fn) if fp8 else t.view(torch.int8)
 
 
-def judge(orc, got, x, q, fp8, s, b, epi, out_dtype, rows=None):
+def judge(orc, got, x, q, fp8, s, b, epi, out_dtype, rows=None, values=False):
+    """`q`: codes [N, K] (widened here), or with `values` the weight's fp32 values [N, K]."""
     m, k = x.shape
     n = q.shape[0]
     rows = np.arange(m, dtype=np.int32) if rows is None else rows
-    wf = code_values(q, fp8)
+    wf = q if values else code_values(q, fp8)
     exact = orc.exact_rows(rows, x, wf, False, k, n, scale=s, bias=b, epilogue=EPI[epi])
     g = got[rows]
     assert np.isfinite(g).all(), "non-finite outputs"

@@ -1,0 +1,114 @@
+"""The product on block scales (GGUF Q8_0: int8 codes, one fp16 scale per 32 consecutive K of an
+output) through the C ABI, against the fp64 truth of the oracle's widened weight W = q · s
+(orc_dequantize, SCALE_BLOCKS: Widen.swift:129-187, one fp32 multiply per weight) at the reference's
+bars (Diagnostic.swift:105-107, CapacityProbes.swift:541-553; max-rel ≤ 2e-2 on bf16 outputs):
+[N, K] codes with GGUF's [N, K/32] fp16 scales, the map's [K, N] with [K/B, N] fp32, the packed
+layout, every epilogue, ragged shapes, and the reference's own entry `linear(…block:…)`."""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import DEV, EPI, bf16_dev, dev, judge
+
+pytestmark = pytest.mark.gpu
+
+_EPI_NAMES = {"none": None, "gelu": "gelu_tanh", "silu": "silu_glu", "situ": "situ_glu"}
+
+
+def q8_problem(orc, m, k, n, block, seed, bias=True):
+    """bf16 X ~ N(0,1); int8 codes [N, K] uniform in [−127, 127]; scales per (output, block of K)
+    U(1e−3, 2e−2) rounded to fp16 (GGUF's `d`); bias N(0, 0.02)."""
+    x = orc.normal_bf16(seed, (m, k))
+    q = orc.uniform_i8(seed + 1, (n, k))
+    d = orc.uniform_f32(seed + 2, (n, k // block), 1e-3, 2e-2).astype(np.float16)
+    b = orc.normal_f32(seed + 3, (n,), 0.0, 0.02) if bias else None
+    return x, q, d, b
+
+
+def widened(orc, q, d, block):
+    """W [K, N] = q · s, the oracle's dequantiser on the map's layout (codes [K, N], scales [K/B, N])."""
+    n, k = q.shape
+    q_kn = np.ascontiguousarray(q.T)
+    s_kn = np.ascontiguousarray(d.T)
+    return orc.dequantize(q_kn.view(np.uint8), orc.INT8, s_kn.view(np.uint16), orc.F16, layout=orc.SCALE_BLOCKS,
+                          columns=n, block_rows=block)
+
+
+def judge_blocks(orc, got, x, q, d, block, b, epi, out_dtype, rows=None):
+    n, k = q.shape
+    w = widened(orc, q, d, block)
+    # judge() widens codes with a per-column scale; here the weight is already q · s: codes = W
+    # transposed to [N, K], scale 1.
+    return judge(orc, got, x, np.ascontiguousarray(w.T), None, np.ones(n, np.float32), b, epi, out_dtype, rows=rows,
+                 values=True)
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn", "packed"])
+@pytest.mark.parametrize("epi", ["none", "gelu", "silu", "situ"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_block_scaled_product(gemm, orc, layout, epi, out_dtype):
+    m, k, n, block = 200, 768, 320, 32
+    x, q, d, b = q8_problem(orc, m, k, n, block, 11)
+    if layout == "nk":
+        w, s = dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16)
+    elif layout == "kn":
+        w, s = dev(np.ascontiguousarray(q.T)).view(torch.int8), dev(np.ascontiguousarray(d.T).astype(np.float32))
+    else:
+        w = gemm.pack_blocks(dev(q).view(torch.int8), dev(d.astype(np.float32)), block, layout="nk",
+                             glu=epi in ("silu", "situ"))
+        s = None
+    y = gemm.product_blocks(bf16_dev(x), w, s, block, layout="kn" if layout == "kn" else "nk", bias=dev(b),
+                            epilogue=_EPI_NAMES[epi], out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    judge_blocks(orc, y.float().cpu().numpy(), x, q, d, block, b, epi, out_dtype)
+
+
+@pytest.mark.parametrize("m,k,n,block", [(1, 64, 64, 32), (37, 1024, 100, 64), (130, 2048, 1000, 128),
+                                         (64, 128, 8, 32), (512, 3072, 3072, 32)])
+def test_block_scaled_shapes(gemm, orc, m, k, n, block):
+    x, q, d, b = q8_problem(orc, m, k, n, block, 23 + m)
+    y = gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16), block,
+                            bias=dev(b), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(m, 64) if m > 64 else None
+    judge_blocks(orc, y.float().cpu().numpy(), x, q, d, block, b, "none", torch.float32, rows=rows)
+
+
+def test_block_scaled_reference_entry(gemm, orc):
+    """`linear(a:int8:…:scales:…:block:…)` as the reference calls it: fp32 activation (rounded to
+    bf16 here), q [K, N] and fp32 scales [K/32, N] at offsets into larger buffers, fp32 C."""
+    m, k, n, block = 96, 512, 192, 32
+    x, q, d, b = q8_problem(orc, m, k, n, block, 5, bias=False)
+    a = dev(orc.bf16_to_f32(x))
+    q_kn = np.ascontiguousarray(q.T)
+    buf = torch.zeros(64 + k * n, dtype=torch.int8, device=DEV)
+    buf[64:] = dev(q_kn).view(torch.int8).reshape(-1)
+    sbuf = torch.zeros(16 + (k // block) * n, dtype=torch.float32, device=DEV)
+    sbuf[16:] = dev(np.ascontiguousarray(d.T).astype(np.float32)).reshape(-1)
+    c = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    gemm.linear(a, int8=buf, scales=sbuf, per_column=False, c=c, m=m, k=k, n=n, weight_offset=64, scales_offset=64,
+                block=block)
+    judge_blocks(orc, c.cpu().numpy(), x, q, d, block, None, "none", torch.float32)
+
+
+def test_block_scaled_refusals(gemm, orc):
+    from siliconed_amd import abi
+    x, q, d, b = q8_problem(orc, 8, 96, 64, 32, 3)
+    with pytest.raises(abi.SQ8Error) as e:      # k not a multiple of 64: the activation tiles
+        gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.astype(np.float32)), 32)
+    assert e.value.status == abi.EUNSUPPORTED
+    x, q, d, b = q8_problem(orc, 8, 128, 64, 16, 3)
+    with pytest.raises(abi.SQ8Error) as e:      # blocks of 16 split an MFMA sub-step
+        gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.astype(np.float32)), 16)
+    assert e.value.status == abi.EUNSUPPORTED
+
+
+def test_block_scaled_bench_size(gemm, orc):
+    """C1's up projection as a Q8_0 weight (4096 × 3072 × 12288, GELU, bf16 out) on 64 sampled rows."""
+    m, k, n, block = 4096, 3072, 12288, 32
+    x, q, d, b = q8_problem(orc, m, k, n, block, 41)
+    w = gemm.pack_blocks(dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16), block)
+    y = gemm.product_blocks(bf16_dev(x), w, bias=dev(b), epilogue="gelu_tanh")
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(m, 64)
+    judge_blocks(orc, y.float().cpu().numpy(), x, q, d, block, b, "gelu", torch.bfloat16, rows=rows)
