@@ -65,7 +65,11 @@ WORKLOADS = {
     "c1_w8a8": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
                 "C1 up-projection on the W8A8 route (ComfyUI int8_linear): fp32 X rotated (groups of 256) and quantized "
                 "per row to int8, int8 x int8 products summed in int32, float(acc)*(s_x*s_w) + bias, fused GELU-tanh, bf16 out"),
+    "c1_q8": (4096, 3072, 12288, "q8_0", "gelu_tanh", "normal",
+              "C1 up-projection on a GGUF Q8_0 weight: int8 codes [N,K] with one fp16 scale per 32 K of each output "
+              "(sq8_linear_blocks), bf16 X, bias + fused GELU-tanh, bf16 out"),
 }
+Q8_BLOCK = 32
 # Workloads whose weight is ComfyUI's convrot: the rotation group. Their activation is fp32 (the
 # reference's rotate_groups reads fp32, TensorGEMM.swift:181-201) and a step is the rotation pass
 # (fp32 → bf16, or fp32 → int8 codes and row scales on the W8A8 route) followed by the product —
@@ -100,8 +104,8 @@ def normal_f32(seed: int, count: int, chunk: int = 1 << 24) -> np.ndarray:
 
 
 def inputs(workload: str):
-    """X bf16 [M, K] (a torch tensor), codes [K, N] (numpy int8) or [N, K] (torch float8_e4m3fn),
-    scales fp32 [N], bias fp32 [N]."""
+    """X bf16 [M, K] (a torch tensor), codes [K, N] (numpy int8) or [N, K] (torch float8_e4m3fn; Q8_0:
+    numpy int8), scales fp32 [N] (Q8_0: fp16 [N, K/32]), bias fp32 [N]."""
     import torch
     M, K, N, wt, epi, xdist, _ = WORKLOADS[workload]
     x = torch.from_numpy(normal_f32(SEEDS["x"], M * K).reshape(M, K))
@@ -116,6 +120,11 @@ def inputs(workload: str):
         q = (np.floor(uniform(SEEDS["w"], K * N) * 255.0) - 127.0).clip(-127, 127).astype(np.int8).reshape(K, N)
         s = (1e-3 + (2e-2 - 1e-3) * uniform(SEEDS["scale"], N)).astype(np.float32)
         return x, q, s, b
+    if wt == "q8_0":
+        # GGUF Q8_0 as published: codes [N, K], one fp16 scale d per 32 consecutive K of an output.
+        q = (np.floor(uniform(SEEDS["w"], K * N) * 255.0) - 127.0).clip(-127, 127).astype(np.int8).reshape(N, K)
+        d = (1e-3 + (2e-2 - 1e-3) * uniform(SEEDS["scale"], N * (K // Q8_BLOCK))).astype(np.float16)
+        return x, q, d.reshape(N, K // Q8_BLOCK), b
     # fp8: w ~ N(0, 0.02) [N, K], s_n = amax_n / 448, q = e4m3fn(RNE(w / s)) (|w / s| ≤ 448: no saturation)
     w = torch.from_numpy(normal_f32(SEEDS["w"], N * K).reshape(N, K)) * 0.02
     s = (w.abs().amax(dim=1) / 448.0).clamp_min(1e-30)
@@ -137,6 +146,8 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0, x32=Non
     a32 = x32[:rows] if group else oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
     if wt == "int8":
         codes, kind = q.view(np.uint8), oracle.INT8            # [K, N], scales per column
+    elif wt == "q8_0":
+        codes, kind = np.ascontiguousarray(q.T).view(np.uint8), oracle.INT8   # [N, K] → [K, N], scales [K/32, N]
     else:
         codes, kind = np.ascontiguousarray(q.view(np.uint8).T), oracle.FP8_E4M3   # [N, K] → [K, N]
     e = {"gelu_tanh": oracle.EPI_GELU_TANH, "silu_glu": oracle.EPI_SILU_GLU}.get(epi, oracle.EPI_NONE)
@@ -146,6 +157,9 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0, x32=Non
         t0 = time.perf_counter()
         if group:
             w = oracle.dequantize_rotated(q, group, s)
+        elif wt == "q8_0":
+            w = oracle.dequantize(codes, kind, np.ascontiguousarray(s.T).view(np.uint16), oracle.F16,
+                                  oracle.SCALE_BLOCKS, columns=N, block_rows=Q8_BLOCK)
         else:
             w = oracle.dequantize(codes, kind, s, oracle.F32, oracle.SCALE_COLUMNS, columns=N)
         t1 = time.perf_counter()
@@ -254,6 +268,7 @@ def main() -> int:
         return dit_block(args)
     M, K, N, wt, epi, _, desc = WORKLOADS[args.workload]
     fp8 = wt == "fp8"
+    q8 = wt == "q8_0"
     glu = epi == "silu_glu"
     qkv = epi == "qkv"
     x, q, s, b = inputs(args.workload)
@@ -261,7 +276,12 @@ def main() -> int:
     sd = torch.from_numpy(s).to(dev)
     bd = torch.from_numpy(b).to(dev)
     ctx = sq.context(0)
-    if fp8:
+    if q8:
+        wd, lay = torch.from_numpy(q).to(dev), "nk"          # [N, K] int8 codes, scales [N, K/32] fp16
+        sd = torch.from_numpy(s).to(dev)
+        if args.layout == "kn":
+            wd, sd, lay = wd.t().contiguous(), sd.t().contiguous(), "kn"
+    elif fp8:
         wd, lay = q.to(dev), "nk"                           # [N, K] e4m3fn codes (packed from [N, K])
         if args.layout == "kn":
             wd, lay = wd.t().contiguous(), "kn"
@@ -273,7 +293,7 @@ def main() -> int:
     if args.layout == "packed":
         torch.cuda.synchronize()
         t_stage = time.perf_counter()
-        wd = ctx.pack(wd, layout=lay, glu=glu)
+        wd = ctx.pack_blocks(wd, sd, Q8_BLOCK, layout=lay, glu=glu) if q8 else ctx.pack(wd, layout=lay, glu=glu)
         torch.cuda.synchronize()
         stage_ms = 1e3 * (time.perf_counter() - t_stage)
     n_out = N // 2 if glu else N
@@ -313,6 +333,11 @@ def main() -> int:
 
         def step():
             ctx.product_qkv(xd, wd, sd, layout=lay, bias=bd, out=outs)
+    elif q8:
+        out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            ctx.product_blocks(xd, wd, sd, Q8_BLOCK, layout=lay, bias=bd, epilogue=epi, out=out)
     else:
         out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
 
@@ -353,7 +378,9 @@ def main() -> int:
     kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
     w8a8 = args.workload in W8A8
     a_bytes = (1 * M * K + 4 * M) if w8a8 else 2 * M * K          # int8 codes + row scales, or bf16
-    algo_bytes = a_bytes + N * K + 4 * N + 4 * N + 2 * M * n_out
+    # Codes, their scales as published (fp32 per column, or Q8_0's fp16 per 32 K), bias, output.
+    w_bytes = N * K + (2 * N * (K // Q8_BLOCK) if q8 else 4 * N)
+    algo_bytes = a_bytes + w_bytes + 4 * N + 2 * M * n_out
     intensity = flops / algo_bytes
     gbs = algo_bytes / (kernel_ms * 1e-3) / 1e9
     peak_mfma = PEAK_INT8_TOPS if w8a8 else PEAK_BF16_TFLOPS

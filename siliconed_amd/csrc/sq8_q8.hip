@@ -77,18 +77,20 @@ int grid_of(int64_t count) {
     return (int)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192);
 }
 
-template <int BM, int NW, int OCC>
+template <int BM, int NW, int OCC, int NB>
 hipError_t dispatch(const GemmArgs &p, int epi, int out, hipStream_t stream) {
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return q8b::launch_q8<BM, NW, OCC, W_INT8, E, O>(p, stream);
+    if (epi == E && out == O) return q8b::launch_q8<BM, NW, OCC, NB, W_INT8, E, O>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
     SQ8_CASE(EPI_GELU, OUT_F32)
-    SQ8_CASE(EPI_SILU_GLU, OUT_BF16)
-    SQ8_CASE(EPI_SILU_GLU, OUT_F32)
-    SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
-    SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    if constexpr (NB == 2) {
+        SQ8_CASE(EPI_SILU_GLU, OUT_BF16)
+        SQ8_CASE(EPI_SILU_GLU, OUT_F32)
+        SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
+        SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    }
 #undef SQ8_CASE
     return hipErrorInvalidValue;
 }
@@ -113,9 +115,11 @@ hipError_t launch_pack_blocks(const uint8_t *w, int wl, int64_t ldw, const void 
 }
 
 hipError_t launch_q8(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream) {
-    if (tile == Q8_64x256) return dispatch<64, 4, 2>(p, epi, out, stream);
-    if (tile == Q8_64x512) return dispatch<64, 8, 1>(p, epi, out, stream);
-    return hipErrorInvalidValue;
+    const bool glu = epi == EPI_SILU_GLU || epi == EPI_SITU_GLU;
+    if (tile == Q8_128x256 && !glu) return dispatch<128, 8, 1, 1>(p, epi, out, stream);
+    if (tile == Q8_128x128 && !glu) return dispatch<128, 4, 2, 1>(p, epi, out, stream);
+    if (tile == Q8_64x512) return dispatch<64, 8, 1, 2>(p, epi, out, stream);
+    return dispatch<64, 4, 2, 2>(p, epi, out, stream);
 }
 
 }  // namespace sq8

@@ -75,16 +75,21 @@ __device__ __forceinline__ void store_block_t(const GemmArgs &p, const f32x16 &x
     wd::flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
 }
 
-template <int BM, int NW, int OCC, int WT, int EPI, int OUT>
+// NB: 32-column blocks per wave — 2 (the wave owns a 64-column slab) or 1 (waves in pairs share a
+// slab, wave w taking block w & 1: half the registers per row block, so twice the rows fit).
+template <int BM, int NW, int OCC, int NB, int WT, int EPI, int OUT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
 gemm_q8_kernel(const GemmArgs p) {
+    static_assert(NB == 1 || NB == 2, "one or two 32-column blocks a wave");
+    static_assert(NB == 2 || NW % 2 == 0, "waves in pairs");
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int FM = BM / 32;
     constexpr int SA = BM * 128;
     constexpr int A_BLOCKS = BM / 8;
     constexpr int A_PER_WAVE = A_BLOCKS / NW;
     static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
-    static_assert(A_PER_WAVE + 5 < 64, "vmcnt budget");
+    constexpr int WLOADS = 2 * NB + 1;  // code loads + the scale load per step
+    static_assert(A_PER_WAVE + WLOADS < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);
     constexpr int LDS_BYTES = NW * REGION > 2 * SA ? NW * REGION : 2 * SA;  // epilogue regions over the stages
 
@@ -96,7 +101,9 @@ gemm_q8_kernel(const GemmArgs p) {
     kern::tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int slabs = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
-    const int slab = tn * NW + wave;
+    constexpr int SLABS_PER_WG = NB == 2 ? NW : NW / 2;
+    const int slab = tn * SLABS_PER_WG + (NB == 2 ? wave : wave >> 1);
+    const int b0 = NB == 2 ? 0 : (wave & 1);  // the wave's first 32-column block in the slab
     const int rslab = slab < slabs ? slab : slabs - 1;  // a wave past the last slab reads the last
     const kern::gbytes Ag = (kern::gbytes)p.a;
     const kern::gbytes Wg = (kern::gbytes)p.w;
@@ -124,14 +131,16 @@ gemm_q8_kernel(const GemmArgs p) {
     // read the same).
     const uint32_t w_base = (uint32_t)((int64_t)rslab * KT * 4096) + lane * 16;
     const uint32_t s_base = (uint32_t)(scales_offset(slabs, KT) + (int64_t)rslab * KT * 512) + (lane & 31) * 16;
-    u32x4 raw[2][4];
+    // raw[B][2·b + kb]: the codes of the wave's block b (0..NB−1 from b0), K block kb of the step.
+    constexpr int NLOAD = 2 * NB;
+    u32x4 raw[2][NLOAD];
     f32x4 sraw[2];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
         const int tt = min(t, KT - 1);
         const kern::gbytes base = Wg + (uint32_t)tt * 4096;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) raw[B][j] = kern::gld<u32x4>(base, w_base + j * 1024);
+        for (int j = 0; j < NLOAD; ++j) raw[B][j] = kern::gld<u32x4>(base, w_base + (2 * b0 + j) * 1024);
         sraw[B] = kern::gld<f32x4>(Wg + (uint32_t)tt * 512, s_base);
     };
 
@@ -142,9 +151,9 @@ gemm_q8_kernel(const GemmArgs p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) xo[par][ks] = swz(32 * par + (lane & 31), 2 * ks + h) - 32 * 128 * par;
 
-    f32x16 acc[2][FM];
+    f32x16 acc[NB][FM];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int bm = 0; bm < FM; ++bm)
 #pragma unroll
@@ -156,18 +165,18 @@ gemm_q8_kernel(const GemmArgs p) {
     issue_a(0, I0{});
     issue_w(0, I0{});
     issue_w(1, I1{});
-    wait_vmcnt<5>();
+    wait_vmcnt<WLOADS>();
     step_barrier();
 
     auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
-        bf16x8 wk[2][2];  // [ks & 1][block]
+        bf16x8 wk[2][NB];  // [ks & 1][block]
         bf16x8 xf[2][FM];
-        f32x16 pp[2][FM];
+        f32x16 pp[NB][FM];
         const f32x4 sv = sraw[P];
         auto widen_ks = [&](auto kc) {
             constexpr int ks = decltype(kc)::value;
-            static_for<0, 2>([&](auto bc) {
+            static_for<0, NB>([&](auto bc) {
                 constexpr int b = decltype(bc)::value;
                 const u32x4 &r = raw[P][2 * b + (ks >> 1)];
                 wk[ks & 1][b] = widen8<WT>(r[2 * (ks & 1)], r[2 * (ks & 1) + 1]);
@@ -195,7 +204,7 @@ gemm_q8_kernel(const GemmArgs p) {
                 issue_w(t + 2, std::integral_constant<int, P>{});
                 __builtin_amdgcn_sched_barrier(0);
             }
-            static_for<0, 2>([&](auto bc) {
+            static_for<0, NB>([&](auto bc) {
                 constexpr int b = decltype(bc)::value;
                 static_for<0, FM>([&](auto bmc) {
                     constexpr int bm = decltype(bmc)::value;
@@ -209,9 +218,9 @@ gemm_q8_kernel(const GemmArgs p) {
             });
             if constexpr ((ks & 1) == 1) {
                 // The block of K ends: its partial sums scaled into the totals.
-                static_for<0, 2>([&](auto bc) {
+                static_for<0, NB>([&](auto bc) {
                     constexpr int b = decltype(bc)::value;
-                    const float s = sv[2 * b + (ks >> 1)];
+                    const float s = NB == 2 ? sv[2 * b + (ks >> 1)] : (b0 ? sv[2 + (ks >> 1)] : sv[ks >> 1]);
                     static_for<0, FM>([&](auto bmc) {
                         constexpr int bm = decltype(bmc)::value;
 #pragma unroll
@@ -221,7 +230,7 @@ gemm_q8_kernel(const GemmArgs p) {
             }
         });
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<5>();
+        wait_vmcnt<WLOADS>();
         step_barrier();
     };
     int t = 0;
@@ -233,39 +242,51 @@ gemm_q8_kernel(const GemmArgs p) {
 
     const bool has_bias = p.bias != nullptr;
     const int n_out = GLU ? p.glu_half : p.N;
-    float bias[2];
-    static_for<0, 2>([&](auto bc) {
-        constexpr int b = decltype(bc)::value;
+    float bias[NB];
+    static_for<0, NB>([&](auto bc) {
+        const int b = b0 + decltype(bc)::value;
         const int oc = GLU ? slab * 32 + (lane & 31) : slab * 64 + 32 * b + (lane & 31);
         const int col = GLU ? min(oc, n_out - 1) + b * p.glu_half : min(oc, n_out - 1);
-        bias[b] = has_bias ? p.bias[col] : 0.0f;
+        bias[decltype(bc)::value] = has_bias ? p.bias[col] : 0.0f;
     });
     wait_vmcnt<0>();
     step_barrier();
 
     uint8_t *region = lds + wave * REGION;
-    static_for<0, FM>([&](auto bmc) {
-        constexpr int bm = decltype(bmc)::value;
-        static_for<0, GLU ? 1 : 2>([&](auto bc) {
-            constexpr int b = decltype(bc)::value;
-            const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
-            if (col0 < n_out)
-                store_block_t<EPI, OUT>(p, acc[b][bm], bias[b], acc[GLU ? 1 : b][bm], bias[GLU ? 1 : b], col0,
-                                        m0 + 32 * bm, n_out, region, lane);
+    if constexpr (NB == 2) {
+        static_for<0, FM>([&](auto bmc) {
+            constexpr int bm = decltype(bmc)::value;
+            static_for<0, GLU ? 1 : 2>([&](auto bc) {
+                constexpr int b = decltype(bc)::value;
+                const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
+                if (col0 < n_out)
+                    store_block_t<EPI, OUT>(p, acc[b][bm], bias[b], acc[GLU ? 1 : b][bm], bias[GLU ? 1 : b], col0,
+                                            m0 + 32 * bm, n_out, region, lane);
+            });
         });
-    });
+    } else {
+        static_assert(!GLU, "a GLU pair needs both blocks of the slab in one wave");
+        const int col0 = slab * 64 + 32 * b0;
+        static_for<0, FM>([&](auto bmc) {
+            constexpr int bm = decltype(bmc)::value;
+            if (col0 < n_out)
+                store_block_t<EPI, OUT>(p, acc[0][bm], bias[0], acc[0][bm], bias[0], col0, m0 + 32 * bm, n_out, region,
+                                        lane);
+        });
+    }
 }
 
-template <int BM, int NW, int OCC, int WT, int EPI, int OUT>
+template <int BM, int NW, int OCC, int NB, int WT, int EPI, int OUT>
 hipError_t launch_q8(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
     p.tiles_m = (p.M + BM - 1) / BM;
     const int slabs = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
-    p.tiles_n = (slabs + NW - 1) / NW;
+    constexpr int SLABS_PER_WG = NB == 2 ? NW : NW / 2;
+    p.tiles_n = (slabs + SLABS_PER_WG - 1) / SLABS_PER_WG;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_q8_kernel<BM, NW, OCC, WT, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_q8_kernel<BM, NW, OCC, NB, WT, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
