@@ -35,7 +35,7 @@ SOURCES = [
     ("sq8_convrot.hip", "sq8_convrot", []),
     ("sq8_w8a8.hip", "sq8_w8a8", []),
     ("sq8_i8_inst.hip", "sq8_i8_inst", []),
-    ("sq8_q8.hip", "sq8_q8", []),
+    ("sq8_blocks.hip", "sq8_blocks", []),
     ("sq8_api.hip", "sq8_api", []),
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

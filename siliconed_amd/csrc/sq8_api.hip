@@ -483,13 +483,13 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
     // 128-row tiles of one 32-column block per wave (the codes widened once for twice the rows);
     // the GLU epilogues pair both blocks of a slab in one wave: 64-row tiles.
-    int tile = is_glu(q.epilogue) ? sq8::Q8_64x256 : sq8::Q8_128x256;
+    int tile = is_glu(q.epilogue) ? sq8::BL_64x256 : sq8::BL_128x256;
     const char *force = getenv("SQ8_Q8_TILE");  // measurement knob: "256", "512", "128x256", "128x128"
-    if (force && strcmp(force, "256") == 0) tile = sq8::Q8_64x256;
-    if (force && strcmp(force, "512") == 0) tile = sq8::Q8_64x512;
-    if (force && strcmp(force, "128x256") == 0) tile = sq8::Q8_128x256;
-    if (force && strcmp(force, "128x128") == 0) tile = sq8::Q8_128x128;
-    hipError_t e = sq8::launch_q8(p, tile, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16,
+    if (force && strcmp(force, "256") == 0) tile = sq8::BL_64x256;
+    if (force && strcmp(force, "512") == 0) tile = sq8::BL_64x512;
+    if (force && strcmp(force, "128x256") == 0) tile = sq8::BL_128x256;
+    if (force && strcmp(force, "128x128") == 0) tile = sq8::BL_128x128;
+    hipError_t e = sq8::launch_blocks_product(p, tile, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16,
                                   ctx->stream);
     if (e != hipSuccess) return hip_status(e);
     if (gpu_seconds) {

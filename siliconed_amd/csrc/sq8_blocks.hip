@@ -1,9 +1,9 @@
-// sq8_q8.hip — codes with a scale per block of rows and column (GGUF Q8_0): the packing into the
+// sq8_blocks.hip — codes with a scale per block of rows and column (GGUF Q8_0): the packing into the
 // packed Q8 layout (codes in the block-aligned K order, then the scales per step and column, widened
-// to fp32) and the product's instantiations (sq8_q8_kernel.h).
+// to fp32) and the product's instantiations (sq8_blocks_kernel.h).
 #include <hip/hip_fp16.h>
 
-#include "sq8_q8_kernel.h"
+#include "sq8_blocks_kernel.h"
 
 namespace sq8 {
 
@@ -80,7 +80,7 @@ int grid_of(int64_t count) {
 template <int BM, int NW, int OCC, int NB>
 hipError_t dispatch(const GemmArgs &p, int epi, int out, hipStream_t stream) {
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return q8b::launch_q8<BM, NW, OCC, NB, W_INT8, E, O>(p, stream);
+    if (epi == E && out == O) return blk::launch_blocks_product<BM, NW, OCC, NB, W_INT8, E, O>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
@@ -114,11 +114,11 @@ hipError_t launch_pack_blocks(const uint8_t *w, int wl, int64_t ldw, const void 
     return hipGetLastError();
 }
 
-hipError_t launch_q8(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream) {
+hipError_t launch_blocks_product(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream) {
     const bool glu = epi == EPI_SILU_GLU || epi == EPI_SITU_GLU;
-    if (tile == Q8_128x256 && !glu) return dispatch<128, 8, 1, 1>(p, epi, out, stream);
-    if (tile == Q8_128x128 && !glu) return dispatch<128, 4, 2, 1>(p, epi, out, stream);
-    if (tile == Q8_64x512) return dispatch<64, 8, 1, 2>(p, epi, out, stream);
+    if (tile == BL_128x256 && !glu) return dispatch<128, 8, 1, 1>(p, epi, out, stream);
+    if (tile == BL_128x128 && !glu) return dispatch<128, 4, 2, 1>(p, epi, out, stream);
+    if (tile == BL_64x512) return dispatch<64, 8, 1, 2>(p, epi, out, stream);
     return dispatch<64, 4, 2, 2>(p, epi, out, stream);
 }
 

@@ -1,4 +1,4 @@
-// sq8_q8_kernel.h — the gfx950 product on codes with a scale per block of rows and column (GGUF
+// sq8_blocks_kernel.h — the gfx950 product on codes with a scale per block of rows and column (GGUF
 // Q8_0: int8 q [K, N], fp32 s [K/B, N], B = 32 or a multiple of it):
 //
 //     C = act(A · W + b),  W[k, n] = q[k, n] · s[k / B, n]
@@ -34,7 +34,7 @@
 #include "sq8_wdirect_kernel.h"
 
 namespace sq8 {
-namespace q8b {
+namespace blk {
 
 using wd::BK;
 using wd::glb_ptr;
@@ -79,7 +79,7 @@ __device__ __forceinline__ void store_block_t(const GemmArgs &p, const f32x16 &x
 // slab, wave w taking block w & 1: half the registers per row block, so twice the rows fit).
 template <int BM, int NW, int OCC, int NB, int WT, int EPI, int OUT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
-gemm_q8_kernel(const GemmArgs p) {
+gemm_blocks_kernel(const GemmArgs p) {
     static_assert(NB == 1 || NB == 2, "one or two 32-column blocks a wave");
     static_assert(NB == 2 || NW % 2 == 0, "waves in pairs");
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -277,7 +277,7 @@ gemm_q8_kernel(const GemmArgs p) {
 }
 
 template <int BM, int NW, int OCC, int NB, int WT, int EPI, int OUT>
-hipError_t launch_q8(const GemmArgs &args, hipStream_t stream) {
+hipError_t launch_blocks_product(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
     p.tiles_m = (p.M + BM - 1) / BM;
@@ -286,9 +286,9 @@ hipError_t launch_q8(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = (slabs + SLABS_PER_WG - 1) / SLABS_PER_WG;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_q8_kernel<BM, NW, OCC, NB, WT, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_blocks_kernel<BM, NW, OCC, NB, WT, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
-}  // namespace q8b
+}  // namespace blk
 }  // namespace sq8

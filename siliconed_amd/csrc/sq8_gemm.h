@@ -62,17 +62,17 @@ bool pack_is_fast(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu)
 hipError_t launch_pack(const uint8_t *w, int wl, int64_t ldw, int k, int n, bool glu, uint8_t *out,
                        hipStream_t stream);
 
-// Codes with a scale per block of rows and column (GGUF Q8_0; sq8_q8.hip): the packed Q8 layout
+// Codes with a scale per block of rows and column (GGUF Q8_0; sq8_blocks.hip): the packed Q8 layout
 // (codes in block-aligned K order, then fp32 scales per step and column) and its product, int8
-// codes, K a multiple of 64, A aligned for 16-byte loads. `tile`: Q8_64x256 (two workgroups per CU),
-// Q8_64x512 (one), Q8_128x256 / Q8_128x128 (eight waves of one 32-column block each, one or two
-// workgroups per CU; not for GLU epilogues, which then take Q8_64x256). Scales [K/B, N] for W_KN codes, [N, K/B] for W_NK; B a multiple of 32
+// codes, K a multiple of 64, A aligned for 16-byte loads. `tile`: BL_64x256 (two workgroups per CU),
+// BL_64x512 (one), BL_128x256 / BL_128x128 (eight waves of one 32-column block each, one or two
+// workgroups per CU; not for GLU epilogues, which then take BL_64x256). Scales [K/B, N] for W_KN codes, [N, K/B] for W_NK; B a multiple of 32
 // dividing K; scale dtype numbered as the C ABI's (fp32, bf16, fp16).
-enum Q8Tile { Q8_64x256 = 0, Q8_64x512 = 1, Q8_128x256 = 2, Q8_128x128 = 3 };
+enum BlocksTile { BL_64x256 = 0, BL_64x512 = 1, BL_128x256 = 2, BL_128x128 = 3 };
 int64_t packed_blocks_bytes(int k, int n, bool glu);
 hipError_t launch_pack_blocks(const uint8_t *w, int wl, int64_t ldw, const void *scale, int scale_dtype, int block,
                               int k, int n, bool glu, uint8_t *out, hipStream_t stream);
-hipError_t launch_q8(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
+hipError_t launch_blocks_product(const GemmArgs &p, int tile, int epi, int out, hipStream_t stream);
 
 // Auxiliary kernels (sq8_aux.hip).
 hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t columns, const void *scale,

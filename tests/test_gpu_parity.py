@@ -256,8 +256,9 @@ def test_empty_and_refused(gemm):
     w = torch.zeros((32, 64), dtype=torch.int8, device=DEV)
     s = torch.ones(32, dtype=torch.float32, device=DEV)
     assert gemm.product(x, w, s).shape == (0, 32)
-    with pytest.raises(abi.Unsupported):
-        gemm.linear(x, int8=w, scales=s, per_column=True, c=torch.empty(0, device=DEV), m=0, k=64, n=32, block=32)
+    with pytest.raises(abi.Unsupported):    # block scales take no rotation (the reference's nil pipeline)
+        gemm.linear(x, int8=w, scales=s, per_column=True, c=torch.empty(0, device=DEV), m=0, k=64, n=32, block=32,
+                    rotation=4)
     with pytest.raises(ValueError):
         gemm.product(torch.zeros((4, 63), dtype=torch.bfloat16, device=DEV), w, s)
 
