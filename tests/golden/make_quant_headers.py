@@ -1,9 +1,18 @@
-"""Writes quant_headers.json.gz: the published safetensors headers of the reference's 8-bit
+"""Writes quant_headers.json.gz and gguf_headers.json.gz.
+
+quant_headers.json.gz: the published safetensors headers of the reference's 8-bit
 fixtures (Tests/SiliconedTests/Fixtures/quant/<slug>/header.json — whole headers of real
 checkpoints, pinned there by repository, revision and sha256), ComfyUI's `comfy_quant` texts and
 the other U8 texts of each manifest (what CompactTests.swift:380-406 writes into its sparse files),
 and which published names each manifest holds quantized and which plain. Data only: the headers as published, the texts as
-recorded. Run where the reference is mounted: python tests/golden/make_quant_headers.py
+recorded.
+
+gguf_headers.json.gz: the reference's GGUF fixtures (`*-gguf*/header.json`: version, alignment,
+data start, metadata, tensor infos of real published files) with each manifest's header byte count,
+sha256 and file size and type counts — what lets a test rebuild the published header bytes, check
+them against the sha256, and parse them over a sparse file of the published size.
+
+Run where the reference is mounted: python tests/golden/make_quant_headers.py
 """
 import gzip
 import json
@@ -45,6 +54,21 @@ def main(root="/root/reference/Tests/SiliconedTests/Fixtures/quant"):
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "quant_headers.json.gz")
     with gzip.open(path, "wt") as f:
         json.dump(out, f, sort_keys=True)
+    print(path, os.path.getsize(path))
+    gguf = {}
+    for slug in sorted(os.listdir(root)):
+        if "gguf" not in slug:
+            continue
+        with open(os.path.join(root, slug, "header.json")) as f:
+            header = json.load(f)              # key order kept: the file's order
+        with open(os.path.join(root, slug, "manifest.json")) as f:
+            m = json.load(f)
+        gguf[slug] = {"header": header, "sha256": m["header"]["sha256"], "header_bytes": m["header"]["bytes"],
+                      "file_bytes": m["file_bytes"], "types": m["types"], "quantized": m.get("quantized", []),
+                      "plain": m.get("plain", [])}
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gguf_headers.json.gz")
+    with gzip.open(path, "wt") as f:
+        json.dump(gguf, f)
     print(path, os.path.getsize(path))
 
 

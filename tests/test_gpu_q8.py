@@ -112,3 +112,25 @@ def test_block_scaled_bench_size(gemm, orc):
     torch.cuda.synchronize()
     rows = orc.sample_rows(m, 64)
     judge_blocks(orc, y.float().cpu().numpy(), x, q, d, block, b, "gelu", torch.bfloat16, rows=rows)
+
+
+def test_gguf_q8_0_weight_staged(gemm, orc, tmp_path):
+    """A Q8_0 weight read from a GGUF file (siliconed_amd.gguf_q8) and staged: the same bits as the
+    product on its codes and scales passed directly, and within the bars of the truth."""
+    from siliconed_amd.gguf_q8 import GGUFFile, write
+    m, k, n = 96, 512, 320
+    x, q, d, b = q8_problem(orc, m, k, n, 32, 9)
+    blocks = np.empty((n * k // 32, 34), np.uint8)
+    blocks[:, :2] = d.reshape(-1, 1).view(np.uint8)
+    blocks[:, 2:] = q.reshape(-1, 32).view(np.uint8)
+    path = str(tmp_path / "w.gguf")
+    write(path, {"general.architecture": ("string", "test")}, {"blk.0.w.weight": ("Q8_0", [k, n], blocks.tobytes())})
+    with GGUFFile(path) as g:
+        wp = g.stage("blk.0.w.weight", gemm)
+    got = gemm.product_blocks(bf16_dev(x), wp, bias=dev(b), out_dtype=torch.float32)
+    want = gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16), 32,
+                               bias=dev(b), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    from refgen import bitwise_equal
+    assert bitwise_equal(got.cpu().numpy(), want.cpu().numpy()) == 0
+    judge_blocks(orc, got.cpu().numpy(), x, q, d, 32, b, "none", torch.float32)
