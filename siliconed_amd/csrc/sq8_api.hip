@@ -233,9 +233,11 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
         int tile = sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
-        const char *force = getenv("SQ8_TILE");  // measurement knob: "256", "128", "s64", "s32"
+        const char *force = getenv("SQ8_TILE");  // measurement knob: "256", "128", "64", "32", "s64", "s32"
         if (force && strcmp(force, "256") == 0) tile = sq8::WD_256;
         if (force && strcmp(force, "128") == 0) tile = sq8::WD_128;
+        if (force && strcmp(force, "64") == 0) tile = sq8::WD_64;
+        if (force && strcmp(force, "32") == 0) tile = sq8::WD_32;
         if (force && strcmp(force, "s64") == 0) tile = sq8::WD_SKINNY64;
         if (force && strcmp(force, "s32") == 0) tile = sq8::WD_SKINNY32;
         e = sq8::launch_wdirect(p, tile, wt, wl, epi, out, ctx->stream);

@@ -20,12 +20,19 @@ hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, 
 }
 
 int choose_wd_tile(int M, int N, bool glu) {
-    // 128 × 256 tiles of 64-column slabs (GLU: 32 output columns a slab). Below 96 of them (M = 1024
-    // at N = 3072, where the two kernels tie on MI355X) the skinny kernel's 32-row tiles with K split
-    // over four waves are faster: 5× at M = 1, 1.7× at M = 512.
+    // Tiles of 256 columns (four 64-column slabs; GLU: 32 output columns a slab), as tall as keeps
+    // at least 144 of them — the measured point below which a shorter tile fills the 256 CUs better
+    // than the taller one loses (K = 3072: M = 1024 at N = 3072 runs 64-row tiles at one workgroup a
+    // CU in 28.5 µs against 42.8 in 128-row tiles; M = 512 32-row tiles in 22.7 against 42.9). Below
+    // 144 tiles of 32 rows, the skinny kernel (K split over four waves): 32-row tiles to M = 128,
+    // 64-row above (M = 16: 8.3 µs against 20.2 for 32-row tiles of the main kernel).
     const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
-    const long tiles = (long)((M + 127) / 128) * ((slabs + 3) / 4);
-    return tiles >= 96 ? WD_128 : WD_SKINNY32;
+    const long tn = (slabs + 3) / 4;
+    auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * tn; };
+    if (tiles(128) >= 144) return WD_128;
+    if (tiles(64) >= 144) return WD_64;
+    if (tiles(32) >= 144) return WD_32;
+    return M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
 }
 
 int choose_tile(int M, int N_out, bool glu) {

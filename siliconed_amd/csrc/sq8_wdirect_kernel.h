@@ -251,9 +251,10 @@ gemm_wd_kernel(const GemmArgs p) {
     static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
     static_assert(A_PER_WAVE + 4 < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
-    static_assert(NW * REGION <= 2 * SA, "the epilogue regions fit in the A stages");
+    // The epilogue regions lie over the A stages (both idle by then); short tiles need more than the stages.
+    constexpr int LDS_BYTES = NW * REGION > 2 * SA ? NW * REGION : 2 * SA;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SA];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

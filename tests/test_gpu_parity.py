@@ -453,3 +453,24 @@ def test_residual_product_is_product_then_residual(gemm, orc, m, layout, gated):
     gemm.product_residual(got, bf16_dev(x_), w, dev(s), layout="nk", bias=dev(b), gate=gate)
     torch.cuda.synchronize()
     assert bitwise_equal(got.cpu().numpy(), expect.cpu().numpy()) == 0
+
+
+@pytest.mark.parametrize("m,n,epi,out_dtype", [(1000, 3000, "gelu", torch.bfloat16), (333, 1536, "none", torch.float32),
+                                               (512, 2048, "silu", torch.bfloat16)])
+def test_tile_heights_same_bits(gemm, orc, monkeypatch, m, n, epi, out_dtype):
+    """The weight-direct kernel in 128-, 64- and 32-row tiles (the product's choice by how many tiles
+    fill the CUs): every output the same bits whichever height computes it — each sum runs the same
+    MFMA sequence over K — on ragged shapes, and within the bars of the truth on sampled rows."""
+    k = 512
+    x, q, s, b = problem(orc, m, k, n, False, 31 + m)
+    wp = gemm.pack(weight_tensor(q, False, "nk"), layout="nk", glu=epi == "silu")
+    outs = {}
+    for tile in ("128", "64", "32"):
+        monkeypatch.setenv("SQ8_TILE", tile)
+        y = gemm.product(bf16_dev(x), wp, dev(s), bias=dev(b), out_dtype=out_dtype,
+                         epilogue={"gelu": "gelu_tanh", "none": None, "silu": "silu_glu"}[epi])
+        torch.cuda.synchronize()
+        outs[tile] = y.float().cpu().numpy()
+    monkeypatch.delenv("SQ8_TILE")
+    assert bitwise_equal(outs["64"], outs["128"]) == 0 and bitwise_equal(outs["32"], outs["128"]) == 0
+    judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
