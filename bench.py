@@ -68,8 +68,14 @@ WORKLOADS = {
     "c1_q8": (4096, 3072, 12288, "q8_0", "gelu_tanh", "normal",
               "C1 up-projection on a GGUF Q8_0 weight: int8 codes [N,K] with one fp16 scale per 32 K of each output "
               "(sq8_linear_blocks), bf16 X, bias + fused GELU-tanh, bf16 out"),
+    "c1_f32": (4096, 3072, 12288, "int8", "gelu_tanh", "normal",
+               "C1 up-projection on the fp32 route: fp32 X used whole, not rounded (three exact bf16 parts along K, "
+               "sq8_linear_f32), int8 weight, bias + fused GELU-tanh, bf16 out"),
 }
 Q8_BLOCK = 32
+# Workloads on the fp32 route: the activation fp32, used whole; a step is the split pass and the
+# product on its three parts (3K steps of K), both inside the one sq8_linear_f32 call.
+EXACT = {"c1_f32"}
 # Workloads whose weight is ComfyUI's convrot: the rotation group. Their activation is fp32 (the
 # reference's rotate_groups reads fp32, TensorGEMM.swift:181-201) and a step is the rotation pass
 # (fp32 → bf16, or fp32 → int8 codes and row scales on the W8A8 route) followed by the product —
@@ -143,7 +149,7 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0, x32=Non
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     rows = min(512, M)
     group = ROTATED.get(workload)
-    a32 = x32[:rows] if group else oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
+    a32 = x32[:rows] if x32 is not None else oracle.bf16_to_f32(x_bf16[:rows].view(np.uint16))
     if wt == "int8":
         codes, kind = q.view(np.uint8), oracle.INT8            # [K, N], scales per column
     elif wt == "q8_0":
@@ -180,6 +186,22 @@ def cpu_baseline(workload: str, x_bf16, q, s, b, budget_s: float = 12.0, x32=Non
                    f"repetition; step = widen + GEMM×{M / rows:g}"),
         "ms_per_step": round(1e3 * t_step, 2),
     }
+
+
+def derived_peak(cus: int) -> dict:
+    """The dense bf16 MFMA peak re-derived on this box: CUs × max shader clock × 4096 FLOP per clock per
+    CU (the clock from hipDeviceGetAttribute, hipDeviceAttributeClockRate = 5, in kHz). The roofline
+    uses the published 2.5 PFLOP/s; this is printed beside it."""
+    out = {"cus": cus}
+    try:
+        import ctypes
+        lib = ctypes.CDLL("libamdhip64.so")
+        khz = ctypes.c_int(0)
+        if lib.hipDeviceGetAttribute(ctypes.byref(khz), 5, 0) == 0 and 100_000 <= khz.value <= 10_000_000:
+            out.update({"max_sclk_mhz": khz.value / 1e3, "bf16_dense_tflops": round(cus * khz.value * 1e3 * 4096 / 1e12, 1)})
+    except OSError:
+        pass
+    return out
 
 
 def dit_block(args) -> int:
@@ -329,6 +351,13 @@ def main() -> int:
                 ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
                 if marks:
                     marks[2].record()
+    elif args.workload in EXACT:
+        x32 = normal_f32(SEEDS["x"], M * K).reshape(M, K)
+        x32d = torch.from_numpy(x32).to(dev)
+        out = torch.empty((M, n_out), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            ctx.product(x32d, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out, rounding=False)
     elif qkv:
         outs = tuple(torch.empty((M, N // 3), dtype=torch.bfloat16, device=dev) for _ in range(3))
 
@@ -378,7 +407,8 @@ def main() -> int:
     tflops = flops / (step_ms * 1e-3) / 1e12
     kernel_tflops = flops / (kernel_ms * 1e-3) / 1e12
     w8a8 = args.workload in W8A8
-    a_bytes = (1 * M * K + 4 * M) if w8a8 else 2 * M * K          # int8 codes + row scales, or bf16
+    # int8 codes + row scales, fp32 (the fp32 route), or bf16
+    a_bytes = (1 * M * K + 4 * M) if w8a8 else 4 * M * K if args.workload in EXACT else 2 * M * K
     # Codes, their scales as published (fp32 per column, or Q8_0's fp16 per 32 K), bias, output.
     w_bytes = N * K + (2 * N * (K // Q8_BLOCK) if q8 else 4 * N)
     algo_bytes = a_bytes + w_bytes + 4 * N + 2 * M * n_out
@@ -395,6 +425,9 @@ def main() -> int:
                      "flops": flops, "intensity_flop_per_byte": round(intensity, 1),
                      "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5),
                      "mfma_bound_ms": round(flops / (peak_mfma * 1e12) * 1e3, 5)})
+    if args.workload in EXACT:
+        # Three bf16 parts per fp32 value: the MFMAs do three times the product's FLOPs.
+        roofline.update({"mfma_flops": 3 * flops, "mfma_bound_ms": round(3 * flops / (peak_mfma * 1e12) * 1e3, 5)})
 
     props = torch.cuda.get_device_properties(0)
     metric = ("TFLOP/s and % bf16 MFMA peak, int8-weight GEMM 4096x3072x12288 on 1 MI355X" if args.workload == "c1_up"
@@ -411,7 +444,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8" if w8a8 else "bf16",
+        "dtype": "int8" if w8a8 else "f32" if args.workload in EXACT else "bf16",
         "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}",
         "config": {"workload": f"{args.workload}: {desc}", "M": M, "K": K, "N": N, "weight_type": wt,
                    "weight_layout": args.layout.upper(),
@@ -422,7 +455,8 @@ def main() -> int:
         "kernel_ms": round(kernel_ms, 5),
         "roofline": roofline,
         **({"activation_pass": rotation} if rotation else {}),
-        "device": {"name": props.name, "cus": props.multi_processor_count},
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "peak_derived": derived_peak(props.multi_processor_count)},
     }
     if not args.no_cpu:
         xb = x.view(torch.int16).numpy()

@@ -120,6 +120,28 @@ int sq8_linear(sq8_ctx *ctx,
                void *c, int c_dtype, int64_t ldc,
                int m, int k, int n, double *gpu_seconds);
 
+/* **The fp32 route**: the product on an fp32 activation used whole, not rounded — the reference's
+ * `submit` on fp32 A (`linear_int8` and the `blocks` pipeline with fp32 operands, TensorGEMM.swift:125-135,
+ * 296-360), judged by its fp32 bar (≤ 1e-5 per channel, Diagnostic.swift:105). Each value is split into three
+ * bf16 parts hi + mid + lo = x along K (each the top 16 bits of what the one before leaves: 24 significant bits
+ * in three parts of 8, none rounded; all normal for |x| ≥ 2^-103), so every product with a code is exact and
+ * the sums are fp32: three times the MFMA work of the rounded route. K a multiple of 64.
+ *   `group` ≠ 0: convrot, A rotated by groups of `group` in fp32 first (TensorGEMM.swift:334-345), as
+ *   sq8_linear_rotated; 0: none.
+ *   `scale_layout` SQ8_SCALE_COLUMNS / SQ8_SCALE_TENSOR: fp32 scales (`scale_dtype` SQ8_F32, `block` 0),
+ *   the weight int8 or fp8 as sq8_linear takes it (packed, [N, K], or [K, N] repacked);
+ *   SQ8_SCALE_BLOCKS: int8 codes with one scale per `block` rows of K and column as sq8_linear_blocks
+ *   takes them (no rotation).
+ * Other arguments as sq8_linear. Replaces: TensorGEMM.linear(a:int8:…) with `rounding` nil
+ * (TensorGEMM.swift:264-290). */
+int sq8_linear_f32(sq8_ctx *ctx,
+                   const float *a, int64_t lda, int group,
+                   const void *w, int w_dtype, int w_layout, int64_t ldw,
+                   const void *scale, int scale_dtype, int scale_layout, int block,
+                   const float *bias, int epilogue,
+                   void *c, int c_dtype, int64_t ldc,
+                   int m, int k, int n, double *gpu_seconds);
+
 /* Bytes of the packed layout of a weight of k × n codes (GLU: n = 2h, the halves paired).
  * Replaces: the reserve plan's size of the staged integers (WeightProducts.int8Plan,
  * Sources/Siliconed/WeightProducts.swift:535-600). */

@@ -67,6 +67,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "orc_situ": (D, [D, D]),
         "orc_sample_rows": (None, [I, I, P]),
         "orc_exact_rows": (None, [P, I, P, I64, P, I, I64, I, I, P, P, I, P]),
+        "orc_exact_rows_f32": (None, [P, I, P, I64, P, I, I64, I, I, P, P, I, P]),
         "orc_channel_error": (D, [P, P, I, I, P, P]),
         "orc_linear_f32": (None, [P, I64, P, I64, I, I, I, P, I, P, I64, I]),
         "orc_epilogue_f32": (None, [P, I64, I, I, P, I, P, I64, I]),
@@ -241,11 +242,13 @@ def exact_rows(rows: np.ndarray, a_bf16: np.ndarray, w: np.ndarray, w_kn: bool, 
                epilogue: int = EPI_NONE) -> np.ndarray:
     """fp64 rows of act(A·W·diag(s) + b): DiagnosticProbes.swift:82-178 (+ the epilogue in double).
 
-    `w` fp32: [K, N] if w_kn else [N, K] (raw codes as floats with `scale`, or dequantized with
-    scale None). Returns [len(rows), n_out] float64.
+    `a_bf16`: bf16 bits (uint16), or fp32 values taken whole. `w` fp32: [K, N] if w_kn else [N, K]
+    (raw codes as floats with `scale`, or dequantized with scale None). Returns [len(rows), n_out]
+    float64.
     """
     rows = np.ascontiguousarray(rows, dtype=np.int32)
-    a_bf16 = np.ascontiguousarray(a_bf16, dtype=np.uint16)
+    f32 = a_bf16.dtype == np.float32      # an fp32 A taken whole (the fp32 route's truth)
+    a_bf16 = np.ascontiguousarray(a_bf16, dtype=np.float32 if f32 else np.uint16)
     w = np.ascontiguousarray(w, dtype=np.float32)
     glu = epilogue in (EPI_SILU_GLU, EPI_SITU_GLU)
     n_out = n // 2 if glu else n
@@ -253,7 +256,8 @@ def exact_rows(rows: np.ndarray, a_bf16: np.ndarray, w: np.ndarray, w_kn: bool, 
     sc = None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)
     bi = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
     ldw = w.shape[1]
-    lib().orc_exact_rows(_p(rows), rows.size, _p(a_bf16), a_bf16.shape[1], _p(w), int(w_kn), ldw, k, n,
+    (lib().orc_exact_rows_f32 if f32 else lib().orc_exact_rows)(
+                         _p(rows), rows.size, _p(a_bf16), a_bf16.shape[1], _p(w), int(w_kn), ldw, k, n,
                          _p(sc), _p(bi), epilogue, _p(out))
     return out
 

@@ -347,15 +347,12 @@ static double epilogue_one(int epilogue, const double *row, int j, int h) {
     }
 }
 
-void orc_exact_rows(const int *rows, int nrows, const uint16_t *a, int64_t lda, const float *w,
-                    int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
-                    int epilogue, double *out) {
+/* The sampled rows of A, widened to double ([nrows, k]), against W: the probe's sums in double. */
+static void exact_from_rows(double *arow, int nrows, const float *w, int w_kn, int64_t ldw, int k, int n,
+                            const float *scale, const float *bias, int epilogue, double *out) {
     int glu = epilogue == ORC_EPI_SILU_GLU || epilogue == ORC_EPI_SITU_GLU;
     int h = glu ? n / 2 : n;
     double *prod = (double *)calloc((size_t)nrows * n, sizeof(double));
-    double *arow = (double *)malloc((size_t)nrows * k * sizeof(double));
-    for (int r = 0; r < nrows; ++r)
-        for (int kk = 0; kk < k; ++kk) arow[(size_t)r * k + kk] = orc_bf16_to_f32(a[(int64_t)rows[r] * lda + kk]);
     if (w_kn) {
         /* W [K, N]: each thread owns a block of columns and streams its K rows once. */
         const int CB = 256;
@@ -393,6 +390,27 @@ void orc_exact_rows(const int *rows, int nrows, const uint16_t *a, int64_t lda, 
         for (int j = 0; j < h; ++j) out[(size_t)r * h + j] = epilogue_one(epilogue, pr, j, h);
     }
     free(prod);
+}
+
+void orc_exact_rows(const int *rows, int nrows, const uint16_t *a, int64_t lda, const float *w,
+                    int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
+                    int epilogue, double *out) {
+    double *arow = (double *)malloc((size_t)nrows * k * sizeof(double));
+    for (int r = 0; r < nrows; ++r)
+        for (int kk = 0; kk < k; ++kk) arow[(size_t)r * k + kk] = orc_bf16_to_f32(a[(int64_t)rows[r] * lda + kk]);
+    exact_from_rows(arow, nrows, w, w_kn, ldw, k, n, scale, bias, epilogue, out);
+    free(arow);
+}
+
+/* The same truth on an fp32 A taken whole (the reference's probe widens its fp32 operand to double,
+ * DiagnosticProbes.swift:79-84): the truth of the fp32 route. */
+void orc_exact_rows_f32(const int *rows, int nrows, const float *a, int64_t lda, const float *w,
+                        int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
+                        int epilogue, double *out) {
+    double *arow = (double *)malloc((size_t)nrows * k * sizeof(double));
+    for (int r = 0; r < nrows; ++r)
+        for (int kk = 0; kk < k; ++kk) arow[(size_t)r * k + kk] = (double)a[(int64_t)rows[r] * lda + kk];
+    exact_from_rows(arow, nrows, w, w_kn, ldw, k, n, scale, bias, epilogue, out);
     free(arow);
 }
 

@@ -97,6 +97,10 @@ void orc_sample_rows(int m, int count, int *rows);
 void orc_exact_rows(const int *rows, int nrows, const uint16_t *a, int64_t lda, const float *w,
                     int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
                     int epilogue, double *out);
+/* As orc_exact_rows on an fp32 A [*, lda] taken whole. */
+void orc_exact_rows_f32(const int *rows, int nrows, const float *a, int64_t lda, const float *w,
+                        int w_kn, int64_t ldw, int k, int n, const float *scale, const float *bias,
+                        int epilogue, double *out);
 /* Per-channel relative error, floored at 1 % of the median norm, NaN = ∞:
  * Sources/Siliconed/DiagnosticJudgement.swift:39-71. got/expected row-major [rows, columns]. */
 double orc_channel_error(const float *got, const double *expected, int rows, int columns,

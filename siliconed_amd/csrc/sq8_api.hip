@@ -100,7 +100,34 @@ struct Product {
     int m, k, n;
     int group;  // convrot: the operand rotated by groups of `group` first (0: none)
     bool residual; const float *gate;  // c (fp32) += gate ⊙ (s ⊙ (A·W) + b), in place
+    bool exact;  // the fp32 route: A fp32 used whole, as three bf16 parts along K (every product exact)
 };
+
+// The fp32 route's operand (the reference's `submit` on an fp32 A, TensorGEMM.swift:296-360): A [m, k] —
+// rotated first by `group` in fp32 when non-zero (rotate_groups, TensorGEMM.swift:334-345) — split into its
+// three bf16 parts hi | mid | lo along K ([m, 3k], hi + mid + lo = x), in the context's scratch: the parts
+// first, the rotated rows after them.
+int stage_parts(sq8_ctx *ctx, const float *a, int64_t lda, int group, int m, int k, const uint16_t **out) {
+    const size_t mk = (size_t)m * (size_t)k;
+    const size_t bytes = mk * 6 + (group != 0 ? mk * 4 : 0);
+    int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
+    if (st != SQ8_OK) return st;
+    uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
+    const float *src = a;
+    int64_t lds = lda;
+    if (group != 0) {
+        // mk·6 bytes in: a multiple of 4 as k is even.
+        float *r = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + mk * 6);
+        hipError_t e = sq8::launch_rotate_groups(a, false, lda, r, false, k, m, k, group, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+        src = r;
+        lds = k;
+    }
+    hipError_t e = sq8::launch_split3(src, lds, y, m, k, ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+    *out = y;
+    return SQ8_OK;
+}
 
 int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (!ctx) return SQ8_EINVAL;
@@ -117,8 +144,11 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
     if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
     if (q.residual && (q.c_dtype != SQ8_F32 || is_glu(q.epilogue) || q.k % 64 != 0)) return SQ8_EUNSUPPORTED;
+    if (q.exact && q.a_dtype != SQ8_F32) return SQ8_EINVAL;
+    if (q.exact && q.k % 64 != 0) return SQ8_EUNSUPPORTED;  // the parts are whole K steps
     // The kernels address A and W with 32-bit byte offsets from their bases.
-    if ((int64_t)q.m * (q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
+    if ((int64_t)q.m * (q.exact ? 3 * (int64_t)q.k : q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k) * 2 >
+            (int64_t)UINT32_MAX ||
         (is_packed(q.w_layout) ? sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue))
                                : (int64_t)(q.w_layout == SQ8_KN ? q.k : q.n) * q.ldw) > (int64_t)UINT32_MAX)
         return SQ8_EUNSUPPORTED;
@@ -134,7 +164,15 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
     }
-    if (q.group != 0) {
+    if (q.exact) {
+        // The fp32 route: the kernels run K' = 3K steps against the weight's K steps, each part facing
+        // the whole weight, so every product is exact and the sums are fp32.
+        const uint16_t *y = nullptr;
+        st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, q.group, q.m, q.k, &y);
+        if (st != SQ8_OK) return st;
+        p.a = y;
+        p.lda = 3 * (int64_t)q.k;
+    } else if (q.group != 0) {
         // convrot: the operand rotated (fp32 butterflies) and rounded to bf16 in one pass, into the
         // context's scratch (TensorGEMMBF16.swift:222-233: rotate_groups, then round_bf16).
         const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
@@ -212,6 +250,10 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     const int cols_per_half = is_glu(q.epilogue) ? q.n / 2 : q.n;
     const bool k_steps = q.k > 0 && (q.k % 64) == 0;
     p.kt = (q.k + 63) / 64;
+    if (q.exact) {
+        p.kt_w = p.kt;  // the weight's steps; the activation has three parts of them
+        p.kt = 3 * p.kt_w;
+    }
     hipError_t e;
     // [K, N] codes in place: repacked per product into the context's buffer when the repack runs near
     // the memory bandwidth (the reference's in-place route, Artifact.swift:443-459, at the speed of
@@ -241,8 +283,8 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         if (force && strcmp(force, "s64") == 0) tile = sq8::WD_SKINNY64;
         if (force && strcmp(force, "s32") == 0) tile = sq8::WD_SKINNY32;
         e = sq8::launch_wdirect(p, tile, wt, wl, epi, out, ctx->stream);
-    } else if (q.residual) {
-        return SQ8_EUNSUPPORTED;  // the residual epilogue runs on the weight-direct kernels only
+    } else if (q.residual || q.exact) {
+        return SQ8_EUNSUPPORTED;  // the residual epilogue and the fp32 route run on the weight-direct kernels only
     } else {
         const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
         const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
@@ -405,6 +447,7 @@ struct Blocks {
     const float *bias; int epilogue;
     void *c; int c_dtype; int64_t ldc;
     int m, k, n;
+    bool exact;  // the fp32 route: A fp32 used whole, as three bf16 parts along K
 };
 
 bool scale_dtype_ok(int t) { return t == SQ8_F32 || t == SQ8_BF16 || t == SQ8_F16; }
@@ -429,7 +472,8 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     if (!packed && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     // Blocks of whole MFMA sub-steps, whole activation tiles, 32-bit offsets into A and the packed codes.
     if (q.block % 32 != 0 || q.k % q.block != 0 || q.k % 64 != 0) return SQ8_EUNSUPPORTED;
-    if ((int64_t)q.m * (q.a_dtype == SQ8_BF16 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
+    if (q.exact && q.a_dtype != SQ8_F32) return SQ8_EINVAL;
+    if ((int64_t)q.m * (q.exact ? 3 * (int64_t)q.k : q.a_dtype == SQ8_BF16 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
         sq8::packed_blocks_bytes(q.k, q.n, is_glu(q.epilogue)) > (int64_t)UINT32_MAX)
         return SQ8_EUNSUPPORTED;
     if (packed && !aligned(q.w, 16)) return SQ8_EINVAL;
@@ -444,7 +488,14 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
         hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
     }
-    if (q.a_dtype == SQ8_F32) {
+    if (q.exact) {
+        // The fp32 route (the reference's `blocks` pipeline on an fp32 A, TensorGEMM.swift:307-320).
+        const uint16_t *y = nullptr;
+        int st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, 0, q.m, q.k, &y);
+        if (st != SQ8_OK) return st;
+        p.a = y;
+        p.lda = 3 * (int64_t)q.k;
+    } else if (q.a_dtype == SQ8_F32) {
         // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
         const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
         int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
@@ -480,6 +531,10 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     p.N = q.n;
     p.K = q.k;
     p.kt = q.k / 64;
+    if (q.exact) {
+        p.kt_w = p.kt;  // the weight's steps; the activation has three parts of them
+        p.kt = 3 * p.kt_w;
+    }
     p.glu_half = is_glu(q.epilogue) ? q.n / 2 : 0;
     const size_t esz = q.c_dtype == SQ8_F32 ? 4 : 2;
     p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
@@ -886,6 +941,36 @@ int sq8_linear_blocks(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, con
     q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
     q.m = m; q.k = k; q.n = n;
     return run_blocks(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_f32(sq8_ctx *ctx, const float *a, int64_t lda, int group, const void *w, int w_dtype, int w_layout,
+                   int64_t ldw, const void *scale, int scale_dtype, int scale_layout, int block, const float *bias,
+                   int epilogue, void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    if (scale_layout == SQ8_SCALE_BLOCKS) {
+        // Block scales take int8 codes and no rotation (the reference's Artifact refuses one there).
+        if (w_dtype != SQ8_INT8 || group != 0) return SQ8_EUNSUPPORTED;
+        Blocks q;
+        memset(&q, 0, sizeof(q));
+        q.a = a; q.a_dtype = SQ8_F32; q.lda = lda;
+        q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+        q.scale = scale; q.scale_dtype = scale_dtype; q.block = block;
+        q.bias = bias; q.epilogue = epilogue;
+        q.c = c; q.c_dtype = c_dtype; q.ldc = ldc;
+        q.m = m; q.k = k; q.n = n;
+        q.exact = true;
+        return run_blocks(ctx, q, gpu_seconds);
+    }
+    if (scale_dtype != SQ8_F32 || block != 0) return SQ8_EINVAL;
+    Product q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = SQ8_F32; q.lda = lda;
+    q.w = w; q.w_dtype = w_dtype; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = static_cast<const float *>(scale); q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    q.group = group;
+    q.exact = true;
+    return run_product(ctx, q, gpu_seconds);
 }
 
 }  // extern "C"

@@ -52,6 +52,32 @@ __global__ void __launch_bounds__(256) round_bf16_kernel(const float *__restrict
         y[i] = (uint16_t)round_bf16(x[i]);
 }
 
+// fp32 → three bf16 parts along K: y[r, k] = hi, y[r, K + k] = mid, y[r, 2K + k] = lo, each part the top
+// 16 bits of what the one before leaves (hi = x truncated to bf16, mid = (x − hi) truncated, lo = x − hi − mid):
+// 24 significant bits in three parts of 8, every difference exact, no part rounded, so hi + mid + lo = x and
+// every product of a part with a code is exact. Every part is a normal bf16 for |x| ≥ 2^−103; an infinity
+// or NaN is its hi part alone. One thread per value of row r, column k.
+__global__ void __launch_bounds__(256) split3_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ y,
+                                                     int64_t rows, int k) {
+    const int64_t count = rows * k;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / k;
+        const int c = (int)(i - r * k);
+        const float v = x[r * ldx + c];
+        const uint32_t u = __float_as_uint(v);
+        uint32_t m = 0, l = 0;
+        if ((u & 0x7f800000u) != 0x7f800000u) {
+            const float r1 = v - __uint_as_float(u & 0xffff0000u);  // the low 16 bits of x: exact
+            m = __float_as_uint(r1) >> 16;
+            l = __float_as_uint(r1 - __uint_as_float(m << 16)) >> 16;  // ≤ 8 bits left: a bf16 value
+        }
+        uint16_t *row = y + r * 3 * (int64_t)k;
+        row[c] = (uint16_t)(u >> 16);
+        row[k + c] = (uint16_t)m;
+        row[2 * k + c] = (uint16_t)l;
+    }
+}
+
 int grid_for(int64_t count) {
     const int64_t blocks = (count + 255) / 256;
     return (int)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192);
@@ -180,6 +206,13 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
     else
         hipLaunchKernelGGL(dequantize_kernel<W_FP8>, dim3(grid_for(count)), dim3(256), 0, stream, codes, rows, columns,
                            scale, scale_dtype, scale_layout, block_rows, first_row, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream) {
+    const int64_t count = rows * k;
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(split3_kernel, dim3(grid_for(count)), dim3(256), 0, stream, x, ldx, y, rows, k);
     return hipGetLastError();
 }
 

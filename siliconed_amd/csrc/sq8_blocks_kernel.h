@@ -129,15 +129,18 @@ gemm_blocks_kernel(const GemmArgs p) {
 
     // Codes: 4 × 16 bytes per lane per step; scales: 16 bytes per lane per step (lanes l and l + 32
     // read the same).
-    const uint32_t w_base = (uint32_t)((int64_t)rslab * KT * 4096) + lane * 16;
-    const uint32_t s_base = (uint32_t)(scales_offset(slabs, KT) + (int64_t)rslab * KT * 512) + (lane & 31) * 16;
+    // The weight's K steps: KT, or kt_w when the activation holds several parts along K that each face
+    // the whole weight (the fp32 route), the weight's step then t modulo kt_w.
+    const int KW = p.kt_w > 0 ? p.kt_w : KT;
+    const uint32_t w_base = (uint32_t)((int64_t)rslab * KW * 4096) + lane * 16;
+    const uint32_t s_base = (uint32_t)(scales_offset(slabs, KW) + (int64_t)rslab * KW * 512) + (lane & 31) * 16;
     // raw[B][2·b + kb]: the codes of the wave's block b (0..NB−1 from b0), K block kb of the step.
     constexpr int NLOAD = 2 * NB;
     u32x4 raw[2][NLOAD];
     f32x4 sraw[2];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
-        const int tt = min(t, KT - 1);
+        const int tt = wd::weight_step(p, min(t, KT - 1));
         const kern::gbytes base = Wg + (uint32_t)tt * 4096;
 #pragma unroll
         for (int j = 0; j < NLOAD; ++j) raw[B][j] = kern::gld<u32x4>(base, w_base + (2 * b0 + j) * 1024);

@@ -31,7 +31,8 @@ struct GemmArgs {
     int tiles_m, tiles_n;   // set by the launcher
     const float *gate;      // EPI_RESIDUAL: per-column gate fp32 [N], or null (1)
     const float *sx;        // W8A8: the activation's row scales fp32 [M] (`a` then holds int8 codes)
-    int kt_w;               // W8A8: K steps of 64 of the packed weight
+    int kt_w;               // W8A8: K steps of 64 of the packed weight; weight-direct kernels: the weight's
+                            // K steps when the activation holds several parts along K (0: kt)
 };
 
 enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };
@@ -80,6 +81,10 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
                              int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out,
                              hipStream_t stream);
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
+// fp32 [rows, k] (leading dimension ldx) → bf16 [rows, 3k]: the three parts hi | mid | lo of each value
+// (each the top 16 bits of what the one before leaves: hi + mid + lo = x, no part rounded), the fp32 route's
+// operand.
+hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream);
 
 // ComfyUI's convrot (sq8_convrot.hip): the activation's rotation x·R by groups of `group` (4, 16,
 // 64 or 256; k a multiple of it), fp32 or bf16 in, fp32 or bf16 (rounded to nearest even) out; and

@@ -64,7 +64,7 @@ gemm_skinny_kernel(const GemmArgs p) {
         constexpr int B = decltype(buf)::value;
         const int t = min(wave + NWK * i, KT - 1);
         const kern::gbytes abase = Ag + (uint32_t)t * (BK * 2);
-        const kern::gbytes wbase = Wg + (uint32_t)t * w_step;
+        const kern::gbytes wbase = Wg + (uint32_t)weight_step(p, t) * w_step;
 #pragma unroll
         for (int j = 0; j < 4; ++j) rw[B][j] = kern::gld<u32x4>(wbase, w_off[j]);
 #pragma unroll

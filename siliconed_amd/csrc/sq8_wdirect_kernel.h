@@ -73,6 +73,17 @@ __device__ __forceinline__ bf16x8 widen8(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(bf16x8, u32x4{o0, o1, o2, o3});
 }
 
+// The weight's K step under activation step t: t itself, or t modulo the weight's kt_w steps when
+// the activation holds up to three parts along K that each face the whole weight (the fp32 route's
+// three bf16 parts of every value, sq8_linear_f32: t < 3·kt_w). Two selects on a wave-uniform value,
+// no branch: a loop here splits the main loop's blocks and the register allocation with them.
+__device__ __forceinline__ int weight_step(const GemmArgs &p, int t) {
+    const int kw = p.kt_w > 0 ? p.kt_w : 0x7fffffff;
+    t -= t >= kw ? kw : 0;
+    t -= t >= kw ? kw : 0;
+    return t;
+}
+
 // Byte offset (K step 0) of the 16 bytes lane `lane`, load j (block j>>1, half j&1) reads for
 // virtual 64-column slab `slab`. Past the edge of an [N, K] weight: the last column of the same half;
 // past the last slab of a packed weight (a tile's waves outnumber the slabs left): the last slab —
@@ -82,7 +93,8 @@ __device__ __forceinline__ uint32_t w_offset(const GemmArgs &p, int slab, int j,
     if constexpr (WL == W_PACKED) {
         const int slabs = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
         const int s = slab < slabs ? slab : slabs - 1;
-        return (uint32_t)(((int64_t)s * p.kt * 4 + j) * 1024 + lane * 16);
+        const int kt = p.kt_w > 0 ? p.kt_w : p.kt;  // the weight's K steps
+        return (uint32_t)(((int64_t)s * kt * 4 + j) * 1024 + lane * 16);
     } else {
         const int b = j >> 1, c = j & 1, h = lane >> 5, nl = lane & 31;
         int n;
@@ -293,7 +305,7 @@ gemm_wd_kernel(const GemmArgs p) {
     u32x4 raw[2][4];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
-        const kern::gbytes base = Wg + (uint32_t)min(t, KT - 1) * w_step;
+        const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
 #pragma unroll
         for (int j = 0; j < 4; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
     };

@@ -95,8 +95,8 @@ def _dev(t: torch.Tensor, what: str) -> int:
 
 
 def _row_major(t: torch.Tensor, what: str) -> int:
-    """Leading dimension of a 2-D tensor whose rows are contiguous."""
-    if t.dim() != 2 or (t.stride(1) != 1 and t.size(1) > 1):
+    """Leading dimension of a 2-D tensor whose rows are contiguous (an empty one: any strides)."""
+    if t.dim() != 2 or (t.stride(1) != 1 and t.size(1) > 1 and t.size(0) > 0):
         raise ValueError(f"{what} must be 2-D with contiguous rows")
     return t.stride(0) if t.size(0) > 1 else max(t.size(1), 1)
 
@@ -154,7 +154,9 @@ class TensorGEMM:
         (TensorGEMM.swift:264-290): C[m, n] = A[m, k] · (q · s), q `[k, n]` (`layout="kn"`, the
         map's) at `weight_offset` bytes into `int8`, its fp32 scales at `scales_offset` bytes into
         `scales` (`n` of them, or one: `per_column` False). `a` fp32 is rounded to bf16 first when
-        `rounding` (the `rounding:` scratch route, TensorGEMMBF16.swift:208-264); `a` bf16 is
+        `rounding` (the `rounding:` scratch route, TensorGEMMBF16.swift:208-264), or with `rounding`
+        False taken whole (the fp32 route, sq8_linear_f32: each value split exactly into three bf16
+        parts, K tripled; rotated in fp32 first with a `rotation`; block scales too); `a` bf16 is
         already rounded. `rotation`: a convrot weight's group (an int, or the reference's
         `(group, scratch, offset, chunk)`, whose scratch and chunk this library replaces with its
         own), the activation rotated by it first (TensorGEMMBF16.swift:222-233). Returns the GPU
@@ -166,8 +168,8 @@ class TensorGEMM:
         `prequantized` = (codes, scales) of `a` already quantized skips that pass.
 
         Routes this library does not take raise `abi.Unsupported` before any work, as the
-        reference's `nil` pipelines send the caller back to the widened route: an fp32 activation
-        not rounded, block scales with a rotation or a W8A8 quantization.
+        reference's `nil` pipelines send the caller back to the widened route: block scales with a
+        rotation or a W8A8 quantization.
 
         `block` = B: scales per block of B rows of K and column (GGUF Q8_0, fp32 `[k / B, n]` at
         `scales_offset`; `per_column` ignored), the product of sq8_linear_blocks.
@@ -175,8 +177,6 @@ class TensorGEMM:
         if block is not None:
             if rotation is not None or quantizing is not None or prequantized is not None or fp8:
                 raise abi.Unsupported(abi.EUNSUPPORTED, "block scales take int8 codes, no rotation, bf16 operands")
-            if a.dtype == torch.float32 and not rounding:
-                raise abi.Unsupported(abi.EUNSUPPORTED, "fp32 activations without bf16 rounding")
             lay = _LAYOUTS[layout]
             epi = _epilogue(epilogue)
             n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
@@ -186,6 +186,16 @@ class TensorGEMM:
                     scales.numel() * 4 < scales_offset + 4 * (k // max(int(block), 1)) * n:
                 raise ValueError("scales must be fp32, [k / block, n] after the offset (a multiple of 4 bytes)")
             secs = ctypes.c_double(0.0)
+            if a.dtype == torch.float32 and not rounding:
+                # The fp32 route on block scales (the reference's `blocks` pipeline on fp32 A).
+                st = abi.load().sq8_linear_f32(self._h, _dev(a, "a"), k, 0, _dev(int8, "int8") + weight_offset,
+                                               abi.INT8, lay, n if lay == abi.KN else k,
+                                               _dev(scales, "scales") + scales_offset, abi.F32, abi.SCALE_BLOCKS,
+                                               int(block), None if bias is None else _dev(bias, "bias"), epi,
+                                               _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                               None if settled else ctypes.byref(secs))
+                abi.check(st, "sq8_linear_f32")
+                return 0.0 if settled else secs.value
             st = abi.load().sq8_linear_blocks(self._h, _dev(a, "a"), _adtype(a), k, _dev(int8, "int8") + weight_offset,
                                               lay, n if lay == abi.KN else k, _dev(scales, "scales") + scales_offset,
                                               abi.F32, int(block), None if bias is None else _dev(bias, "bias"), epi,
@@ -199,8 +209,7 @@ class TensorGEMM:
                 raise abi.Unsupported(abi.EUNSUPPORTED, "W8A8 takes int8 weights")
             return self._w8a8_linear(a, int8, scales, per_column, c, m, k, n, weight_offset, scales_offset, group,
                                      prequantized, settled, layout, bias, epilogue)
-        if a.dtype == torch.float32 and not rounding:
-            raise abi.Unsupported(abi.EUNSUPPORTED, "fp32 activations without bf16 rounding")
+        exact = a.dtype == torch.float32 and not rounding
         lay = _LAYOUTS[layout]
         wd = _wdtype(int8, fp8)
         epi = _epilogue(epilogue)
@@ -215,6 +224,16 @@ class TensorGEMM:
             raise ValueError("the scales' offset must be a multiple of 4 bytes")
         ldw = n if lay == abi.KN else k
         secs = ctypes.c_double(0.0)
+        if exact:
+            # The reference's `submit` on fp32 A: the fp32 route (three exact bf16 parts per value).
+            st = abi.load().sq8_linear_f32(self._h, _dev(a, "a"), k, group, _dev(int8, "int8") + weight_offset, wd, lay,
+                                           ldw, _dev(scales, "scales") + scales_offset, abi.F32,
+                                           abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR, 0,
+                                           None if bias is None else _dev(bias, "bias"), epi,
+                                           _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                           None if settled else ctypes.byref(secs))
+            abi.check(st, "sq8_linear_f32")
+            return 0.0 if settled else secs.value
         args = ((self._h, _dev(a, "a"), _adtype(a), k) + ((group,) if group else ()) +
                 (_dev(int8, "int8") + weight_offset, wd, lay, ldw,
                  _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
@@ -365,10 +384,11 @@ class TensorGEMM:
     def product_blocks(self, x: torch.Tensor, w, scale: Optional[torch.Tensor] = None, block: int = 32, *,
                        layout: str = "nk", bias: Optional[torch.Tensor] = None, epilogue=None,
                        out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
-                       timed: bool = False):
+                       timed: bool = False, rounding: bool = True):
         """y = act(x · Wᵀ + b), W[n, k] = q · s[block of k, n] (GGUF Q8_0: block 32): x [m, k] bf16
-        (or fp32, rounded); W int8 codes [n, k] ("nk", scales [n, k/block]) or [k, n] ("kn",
-        scales [k/block, n]), or a PackedBlocks (scale and block from it)."""
+        (or fp32: rounded, or with `rounding=False` used whole, the fp32 route); W int8 codes [n, k]
+        ("nk", scales [n, k/block]) or [k, n] ("kn", scales [k/block, n]), or a PackedBlocks (scale and
+        block from it)."""
         epi = _epilogue(epilogue)
         m, k = x.shape
         if isinstance(w, PackedBlocks):
@@ -393,6 +413,14 @@ class TensorGEMM:
         if out is None:
             out = torch.empty((m, n_out), dtype=out_dtype, device=x.device)
         secs = ctypes.c_double(0.0)
+        if not rounding and x.dtype == torch.float32:
+            st = abi.load().sq8_linear_f32(self._h, _dev(x, "x"), _row_major(x, "x"), 0, wptr, abi.INT8, lay, ldw,
+                                           sptr, sdt, abi.SCALE_BLOCKS, int(block),
+                                           None if bias is None else _dev(bias, "bias"), epi, _dev(out, "out"),
+                                           _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+                                           ctypes.byref(secs) if timed else None)
+            abi.check(st, "sq8_linear_f32")
+            return (out, secs.value) if timed else out
         st = abi.load().sq8_linear_blocks(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"), wptr, lay, ldw, sptr,
                                           sdt, int(block), None if bias is None else _dev(bias, "bias"), epi,
                                           _dev(out, "out"), _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
@@ -405,10 +433,13 @@ class TensorGEMM:
     def product(self, x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, *, layout: str = "nk",
                 bias: Optional[torch.Tensor] = None, epilogue=None, out: Optional[torch.Tensor] = None,
                 out_dtype: torch.dtype = torch.bfloat16, fp8: Optional[bool] = None,
-                timed: bool = False, rotation: int = 0):
+                timed: bool = False, rotation: int = 0, rounding: bool = True):
         """y = act(s ⊙ (x · Wᵀ) + b) for x [m, k] and W [n, k] (`layout="nk"`, nn.Linear) or
         [k, n] (`"kn"`, the map's). `rotation` = G: a convrot weight, x rotated by groups of G
-        first (y = act(s ⊙ ((x·R) · qᵀ) + b)). Returns y (and the GPU seconds when `timed`)."""
+        first (y = act(s ⊙ ((x·R) · qᵀ) + b)). An fp32 x is rounded to bf16 first (`rounding`, the
+        reference's submitRounded), or with `rounding=False` used whole: the fp32 route (sq8_linear_f32;
+        with a `rotation`, x rotated in fp32 first). Returns y (and the GPU seconds when `timed`)."""
+        exact = not rounding and x.dtype == torch.float32
         epi = _epilogue(epilogue)
         m, k = x.shape
         if isinstance(w, PackedWeight):
@@ -440,6 +471,15 @@ class TensorGEMM:
         elif tuple(out.shape) != (m, n_out):
             raise ValueError("out has the wrong shape")
         secs = ctypes.c_double(0.0)
+        if exact:
+            st = abi.load().sq8_linear_f32(self._h, _dev(x, "x"), _row_major(x, "x"), int(rotation), wptr, wd, lay,
+                                           ldw, _dev(scale, "scale"), abi.F32,
+                                           abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR, 0,
+                                           None if bias is None else _dev(bias, "bias"), epi, _dev(out, "out"),
+                                           _cdtype(out.dtype), _row_major(out, "out"), m, k, n,
+                                           ctypes.byref(secs) if timed else None)
+            abi.check(st, "sq8_linear_f32")
+            return (out, secs.value) if timed else out
         args = ((self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x")) + ((int(rotation),) if rotation else ()) +
                 (wptr, wd, lay, ldw,
                  _dev(scale, "scale"), abi.SCALE_COLUMNS if per_col else abi.SCALE_TENSOR,

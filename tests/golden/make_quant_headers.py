@@ -52,8 +52,8 @@ def main(root="/root/reference/Tests/SiliconedTests/Fixtures/quant"):
         out[slug] = {"header": header, "texts": texts, "group": m.get("group"),
                      "groups": sorted(set(groups)), "plain": sorted(set(plain) - set(groups))}
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "quant_headers.json.gz")
-    with gzip.open(path, "wt") as f:
-        json.dump(out, f, sort_keys=True)
+    with open(path, "wb") as raw, gzip.GzipFile(fileobj=raw, mode="wb", mtime=0) as z:
+        z.write(json.dumps(out, sort_keys=True).encode())
     print(path, os.path.getsize(path))
     gguf = {}
     for slug in sorted(os.listdir(root)):
@@ -67,8 +67,8 @@ def main(root="/root/reference/Tests/SiliconedTests/Fixtures/quant"):
                       "file_bytes": m["file_bytes"], "types": m["types"], "quantized": m.get("quantized", []),
                       "plain": m.get("plain", [])}
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gguf_headers.json.gz")
-    with gzip.open(path, "wt") as f:
-        json.dump(gguf, f)
+    with open(path, "wb") as raw, gzip.GzipFile(fileobj=raw, mode="wb", mtime=0) as z:
+        z.write(json.dumps(gguf).encode())
     print(path, os.path.getsize(path))
 
 

@@ -197,6 +197,62 @@ def test_exact_rows_sampled_are_those_rows(orc):
     assert np.array_equal(orc.exact_rows(rows, a, q, False, k, n), full[rows])
 
 
+def test_exact_rows_of_an_fp32_activation(orc):
+    """The truth on fp32 A taken whole (DiagnosticProbes.swift:79-84 widens A to double): against numpy's
+    float64 product (each term exact, sums within a few ulp of double), and on fp32 values that are bf16
+    values, the same doubles as the bf16 truth."""
+    m, k, n = 40, 96, 24
+    a = orc.normal_f32(8, (m, k))
+    q = orc.uniform_i8(9, (n, k)).astype(np.float32)
+    s = orc.uniform_f32(10, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(11, (n,), 0.0, 0.02)
+    rows = np.arange(m, dtype=np.int32)
+    y = orc.exact_rows(rows, a, q, False, k, n, scale=s, bias=b)
+    want = (a.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64) + b.astype(np.float64)
+    np.testing.assert_allclose(y, want, rtol=1e-13, atol=1e-15)
+    assert np.abs(y - orc.exact_rows(rows, orc.f32_to_bf16(a), q, False, k, n, scale=s, bias=b)).max() > 1e-4
+    bits = orc.f32_to_bf16(a)
+    assert np.array_equal(orc.exact_rows(rows, orc.bf16_to_f32(bits), q, False, k, n, scale=s, bias=b),
+                          orc.exact_rows(rows, bits, q, False, k, n, scale=s, bias=b))
+
+
+def _parts(x):
+    """hi, mid, lo: each the top 16 bits of what the part before leaves (truncation, no rounding)."""
+    top = lambda v: (v.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    hi = top(x)
+    r1 = (x - hi).astype(np.float32)
+    mid = top(r1)
+    r2 = (r1 - mid).astype(np.float32)
+    return hi, mid, top(r2), r1, r2
+
+
+def test_three_bf16_parts_are_exact():
+    """The fp32 route's operand: three bf16 parts whose sum is x exactly (24 significant bits in three
+    parts of 8): every fp32 difference exact, the last remainder already a bf16 value, every part a
+    normal number for |x| ≥ 2^−103, and fp32's largest values kept (rounding hi to nearest would
+    carry 3.4e38 to infinity)."""
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.standard_normal(20000).astype(np.float32),
+                        (rng.standard_normal(20000) * 2.0 ** rng.integers(-103, 127, 20000)).astype(np.float32),
+                        np.float32([1 + 2 ** -23, -(1 - 2 ** -24), 2 ** -103, 3.4028235e38, -3.4e38, 0.0])])
+    x = x[np.isfinite(x)]
+    hi, mid, lo, r1, r2 = _parts(x)
+    d = lambda v: v.astype(np.float64)
+    assert np.array_equal(d(r1), d(x) - d(hi)) and np.array_equal(d(r2), d(r1) - d(mid))
+    assert np.array_equal(lo, r2)                            # the remainder is a bf16 value already
+    assert np.array_equal(d(hi) + d(mid) + d(lo), d(x))
+    tiny, big_enough = np.finfo(np.float32).tiny, np.abs(x) >= 2.0 ** -103
+    assert (~big_enough).sum() > 10                          # the draw reaches below the bound too
+    for part in (mid, lo):
+        nz = part[big_enough & (part != 0)]
+        assert (np.abs(nz) >= tiny).all()                    # no subnormal part for |x| ≥ 2^−103
+    assert np.isfinite(hi).all()
+    # Rounded to nearest even instead, fp32's largest value would carry into infinity.
+    u = np.uint32(np.float32(3.4028235e38).view(np.uint32))
+    rne = np.uint32((int(u) + 0x7FFF + ((int(u) >> 16) & 1)) & 0xFFFF0000).view(np.float32)
+    assert np.isinf(rne) and np.isfinite(_parts(np.float32([3.4028235e38]))[0]).all()
+
+
 def test_sample_rows_visit_every_slice(orc):
     for m, c in [(4096, 64), (65, 64), (64, 64), (1000, 7)]:
         r = orc.sample_rows(m, c)
