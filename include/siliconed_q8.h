@@ -142,6 +142,17 @@ int sq8_linear_f32(sq8_ctx *ctx,
                    void *c, int c_dtype, int64_t ldc,
                    int m, int k, int n, double *gpu_seconds);
 
+/* **The bf16-weight product**: C fp32 [m, n] (leading dimension ldc) = A [m, k] · W, W bf16 [k, n]
+ * (SQ8_KN: `weightIsTransposed`, the forge's layout) or [n, k] (SQ8_NK), no scale, no bias, C written. A fp32
+ * (`a_dtype` SQ8_F32) is used whole — split into three exact bf16 parts as on the fp32 route, every product
+ * exact, the sums fp32 — or bf16 (SQ8_BF16). A plain GEMM: the library GEMM (rocBLAS) runs it.
+ * Replaces: TensorGEMM.linear(a:w:c:m:k:n:weightIsTransposed:) (TensorGEMM.swift:236-254). */
+int sq8_linear_bf16_weight(sq8_ctx *ctx,
+                           const void *a, int a_dtype, int64_t lda,
+                           const void *w, int w_layout, int64_t ldw,
+                           float *c, int64_t ldc,
+                           int m, int k, int n, double *gpu_seconds);
+
 /* Bytes of the packed layout of a weight of k × n codes (GLU: n = 2h, the halves paired).
  * Replaces: the reserve plan's size of the staged integers (WeightProducts.int8Plan,
  * Sources/Siliconed/WeightProducts.swift:535-600). */

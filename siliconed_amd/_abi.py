@@ -50,6 +50,7 @@ SIGNATURES = {
     "sq8_pack_weight": (_I, [_P, _P, _I, _I64, _I, _I, _I, _P]),
     "sq8_linear_f32": (_I, [_P, _P, _I64, _I, _P, _I, _I, _I64, _P, _I, _I, _I, _P, _I, _P, _I, _I64, _I, _I, _I,
                             ctypes.POINTER(ctypes.c_double)]),
+    "sq8_linear_bf16_weight": (_I, [_P, _P, _I, _I64, _P, _I, _I64, _P, _I64, _I, _I, _I, ctypes.POINTER(_D)]),
     "sq8_linear_blocks": (_I, [_P, _P, _I, _I64, _P, _I, _I64, _P, _I, _I, _P, _I, _P, _I, _I64, _I, _I, _I,
                                ctypes.POINTER(ctypes.c_double)]),
     "sq8_packed_blocks_bytes": (_I64, [_I, _I, _I]),

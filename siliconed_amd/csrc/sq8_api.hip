@@ -4,6 +4,7 @@
 #include "siliconed_q8.h"
 
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -21,6 +22,7 @@ struct sq8_ctx {
     size_t scratch_bytes;
     void *wpack;            // [K, N] codes repacked for the weight-direct kernels, per product
     size_t wpack_bytes;
+    rocblas_handle blas;    // the bf16-weight product's library GEMM (created on its first call)
 };
 
 namespace {
@@ -560,6 +562,84 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     return SQ8_OK;
 }
 
+// The bf16-weight product (TensorGEMM.swift:236-254, `matmul2d` float × bfloat): C fp32 [m, n] = A · W,
+// W bf16 [k, n] (SQ8_KN) or [n, k] (SQ8_NK). A plain GEMM, so the library GEMM (rocBLAS gemm_ex: bf16
+// operands, fp32 sums) takes it; an fp32 A is split into its three bf16 parts first (stage_parts) and the
+// three products summed into C (beta 0, 1, 1): every product exact, the sums fp32.
+int blas_status(rocblas_status s) {
+    switch (s) {
+    case rocblas_status_success: return SQ8_OK;
+    case rocblas_status_invalid_size:
+    case rocblas_status_invalid_value:
+    case rocblas_status_invalid_pointer:
+    case rocblas_status_invalid_handle: return SQ8_EINVAL;
+    case rocblas_status_not_implemented: return SQ8_EUNSUPPORTED;
+    case rocblas_status_memory_error: return hip_status(hipErrorOutOfMemory);
+    default: return hip_status(hipErrorLaunchFailure);
+    }
+}
+
+int run_bf16_weight(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_layout, int64_t ldw,
+                    float *c, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    if (!ctx) return SQ8_EINVAL;
+    if (a_dtype != SQ8_BF16 && a_dtype != SQ8_F32) return SQ8_EUNSUPPORTED;
+    if (w_layout != SQ8_KN && w_layout != SQ8_NK) return SQ8_EUNSUPPORTED;
+    if (m < 0 || k < 0 || n < 0) return SQ8_EINVAL;
+    if (gpu_seconds) *gpu_seconds = 0.0;
+    if (m == 0 || n == 0) return SQ8_OK;
+    if (!a || !w || !c) return SQ8_EINVAL;
+    if (lda < k || ldw < (w_layout == SQ8_KN ? n : k) || ldc < n) return SQ8_EINVAL;
+    // The library GEMM's sizes and leading dimensions are 32-bit.
+    if (lda > INT32_MAX / 3 || ldw > INT32_MAX || ldc > INT32_MAX) return SQ8_EUNSUPPORTED;
+    DeviceScope scope(ctx->device);
+    if (scope.error != hipSuccess) return hip_status(scope.error);
+    if (!ctx->blas) {
+        rocblas_status bs = rocblas_create_handle(&ctx->blas);
+        if (bs != rocblas_status_success) { ctx->blas = nullptr; return blas_status(bs); }
+    }
+    rocblas_status bs = rocblas_set_stream(ctx->blas, ctx->stream);
+    if (bs != rocblas_status_success) return blas_status(bs);
+    if (gpu_seconds) {
+        hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    if (k == 0) {
+        hipError_t e = hipMemset2DAsync(c, (size_t)ldc * 4, 0, (size_t)n * 4, (size_t)m, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    } else {
+        const uint16_t *parts = static_cast<const uint16_t *>(a);
+        int64_t ldp = lda;
+        int count = 1;
+        if (a_dtype == SQ8_F32) {
+            int st = stage_parts(ctx, static_cast<const float *>(a), lda, 0, m, k, &parts);
+            if (st != SQ8_OK) return st;
+            ldp = 3 * (int64_t)k;
+            count = 3;
+        }
+        // Row-major C [m, n] is column-major Cᵀ [n, m]: Cᵀ = op(W) · Aᵀ, W [k, n] row-major being the
+        // column-major n × k matrix Wᵀ itself (no transpose), W [n, k] its transpose.
+        const float one = 1.0f, zero = 0.0f;
+        for (int part = 0; part < count; ++part) {
+            bs = rocblas_gemm_ex(ctx->blas, w_layout == SQ8_KN ? rocblas_operation_none : rocblas_operation_transpose,
+                                 rocblas_operation_none, n, m, k, &one, w, rocblas_datatype_bf16_r, (rocblas_int)ldw,
+                                 parts + (int64_t)part * k, rocblas_datatype_bf16_r, (rocblas_int)ldp,
+                                 part == 0 ? &zero : &one, c, rocblas_datatype_f32_r, (rocblas_int)ldc, c,
+                                 rocblas_datatype_f32_r, (rocblas_int)ldc, rocblas_datatype_f32_r,
+                                 rocblas_gemm_algo_standard, 0, 0);
+            if (bs != rocblas_status_success) return blas_status(bs);
+        }
+    }
+    if (gpu_seconds) {
+        hipError_t e = hipEventRecord(ctx->end, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->end);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->begin, ctx->end);
+        if (e != hipSuccess) return hip_status(e);
+        *gpu_seconds = (double)ms * 1e-3;
+    }
+    return SQ8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -612,6 +692,7 @@ int sq8_destroy(sq8_ctx *ctx) {
     if (e != hipSuccess) st = hip_status(e);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->wpack) (void)hipFree(ctx->wpack);
+    if (ctx->blas) (void)rocblas_destroy_handle(ctx->blas);
     (void)hipEventDestroy(ctx->begin);
     (void)hipEventDestroy(ctx->end);
     delete ctx;
@@ -971,6 +1052,11 @@ int sq8_linear_f32(sq8_ctx *ctx, const float *a, int64_t lda, int group, const v
     q.group = group;
     q.exact = true;
     return run_product(ctx, q, gpu_seconds);
+}
+
+int sq8_linear_bf16_weight(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const void *w, int w_layout,
+                           int64_t ldw, float *c, int64_t ldc, int m, int k, int n, double *gpu_seconds) {
+    return run_bf16_weight(ctx, a, a_dtype, lda, w, w_layout, ldw, c, ldc, m, k, n, gpu_seconds);
 }
 
 }  // extern "C"

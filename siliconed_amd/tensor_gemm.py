@@ -244,6 +244,40 @@ class TensorGEMM:
         abi.check(getattr(abi.load(), name)(*args), name)
         return 0.0 if settled else secs.value
 
+    def linear_bf16_weight(self, a: torch.Tensor, *, w: torch.Tensor, c: torch.Tensor, m: int, k: int, n: int,
+                           weight_is_transposed: bool) -> float:
+        """`linear(a:w:c:m:k:n:weightIsTransposed:)` (TensorGEMM.swift:236-254): C fp32 [m, n] = A [m, k] · W,
+        W bf16 `[k, n]` when `weight_is_transposed` (the forge's layout), `[n, k]` otherwise, all row-major
+        from offset 0. A fp32 (used whole: three exact bf16 parts) or bf16. Returns the GPU seconds."""
+        if w.dtype != torch.bfloat16 or c.dtype != torch.float32:
+            raise ValueError("w must be bf16 and c fp32")
+        if a.numel() < m * k or w.numel() < k * n or c.numel() < m * n:
+            raise ValueError("a, w or c smaller than m × k, k × n, m × n")
+        secs = ctypes.c_double(0.0)
+        st = abi.load().sq8_linear_bf16_weight(self._h, _dev(a, "a"), _adtype(a), k, _dev(w, "w"),
+                                               abi.KN if weight_is_transposed else abi.NK,
+                                               n if weight_is_transposed else k, _dev(c, "c"), n, m, k, n,
+                                               ctypes.byref(secs))
+        abi.check(st, "sq8_linear_bf16_weight")
+        return secs.value
+
+    def product_bf16_weight(self, x: torch.Tensor, w: torch.Tensor, *, layout: str = "nk",
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """y fp32 [m, n] = x · Wᵀ for W bf16 [n, k] (`"nk"`, nn.Linear) or x · W for W [k, n] (`"kn"`);
+        x fp32 (used whole) or bf16. No scale, no bias: the bf16-weight product."""
+        m, k = x.shape
+        lay = _LAYOUTS[layout]
+        if w.dtype != torch.bfloat16 or w.dim() != 2 or (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
+            raise ValueError(f"w must be bf16 [n, k] or [k, n] matching x [{m}, {k}]")
+        n = w.shape[0] if lay == abi.NK else w.shape[1]
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+        st = abi.load().sq8_linear_bf16_weight(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"), _dev(w, "w"), lay,
+                                               _row_major(w, "w"), _dev(out, "out"), _row_major(out, "out"), m, k, n,
+                                               None)
+        abi.check(st, "sq8_linear_bf16_weight")
+        return out
+
     def _w8a8_linear(self, a, int8, scales, per_column, c, m, k, n, weight_offset, scales_offset, group, prequantized,
                      settled, layout, bias, epilogue) -> float:
         lay = _LAYOUTS[layout]
