@@ -11,12 +11,12 @@
 // of a 64-code step, h = lane ÷ 32), whose k sets the activation fragments match (row r of the A
 // stage is 128 codes; sub-step s of lane half h reads its 16 bytes at 64·(s >> 1) + 32h + 16·(s & 1)).
 //
-// Activation: a 2-stage LDS ring of [BM][128] int8 tiles filled by direct global→LDS loads, rows
+// Activation: a 2- or 3-stage LDS ring of [BM][128] int8 tiles filled by direct global→LDS loads, rows
 // XOR-swizzled as the bf16 kernel's. The activation rows must hold whole steps: k_pad = a multiple
 // of 128 codes, zero past k (the quantization pass writes them so); the weight's last packed step is
 // reused past its end when the packed steps are odd (times zero codes).
 //
-// Per step t (two workgroups per CU, ≤ 256 registers a wave): issue A(t+1), the MFMAs of the four
+// Per step t (two workgroups per CU, ≤ 256 registers a wave): issue A(t+NA−1), the MFMAs of the four
 // sub-steps with the fragments of s+1 read during s, W(t+2)'s first packed step into raw[t&1] once
 // sub-step 1 has read it, its second once sub-step 3 has; wait until A(t+1) and W(t+1) landed;
 // barrier.
@@ -53,7 +53,9 @@ __device__ __forceinline__ uint32_t w_offset_i8(const GemmArgs &p, int slab, int
     }
 }
 
-template <int BM, int NW, int WL, int EPI, int OUT>
+// NA: activation stages in the LDS ring (2: A(t+1) loads during step t; 3: A(t+2), one more step of
+// memory latency covered, 3·BM·128 bytes of LDS).
+template <int BM, int NW, int WL, int EPI, int OUT, int NA>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(2, 2)))
 gemm_i8_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -61,12 +63,16 @@ gemm_i8_kernel(const GemmArgs p) {
     constexpr int SA = BM * 128;          // bytes per A stage: BM rows of 128 codes
     constexpr int A_BLOCKS = BM / 8;      // 1 KB (8-row) blocks per stage
     constexpr int A_PER_WAVE = A_BLOCKS / NW;
+    static_assert(NA == 2 || NA == 3, "two or three activation stages");
     static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
-    static_assert(A_PER_WAVE + 8 < 64, "vmcnt budget");
+    static_assert(2 * A_PER_WAVE + 16 < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);
     static_assert(NW * REGION <= 2 * SA, "the epilogue regions fit in the A stages");
+    // Loads a wave may leave in flight at the end of step t, A(t+1) and W(t+1) landed: W(t+2), and with
+    // three stages A(t+2) (issued in step t, before W(t+2)).
+    constexpr int IN_FLIGHT = 8 + (NA == 3 ? A_PER_WAVE : 0);
 
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SA];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NA * SA];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -130,19 +136,22 @@ gemm_i8_kernel(const GemmArgs p) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
 
-    auto step = [&](int t, auto par) {
+    // Step t: the weight's register buffer P = t mod 2, the activation's stage S = t mod NA.
+    auto step = [&](int t, auto par, auto stage) {
         constexpr int P = decltype(par)::value;
+        constexpr int S = decltype(stage)::value;
         i32x4 xf[2][FM];
         auto read_x = [&](auto sc) {
             constexpr int s = decltype(sc)::value;
             static_for<0, FM>([&](auto bmc) {
                 constexpr int bm = decltype(bmc)::value;
-                xf[s & 1][bm] = __builtin_bit_cast(i32x4, kern::lds_load_frag(lds + P * SA + 32 * 128 * bm, xo[bm & 1][s]));
+                xf[s & 1][bm] = __builtin_bit_cast(i32x4, kern::lds_load_frag(lds + S * SA + 32 * 128 * bm, xo[bm & 1][s]));
             });
         };
         __builtin_amdgcn_sched_barrier(0);
         read_x(I0{});
-        issue_a(t + 1, std::integral_constant<int, 1 - P>{});
+        // Into the stage read during step t − 1 (the barrier that ended it saw every wave's reads).
+        issue_a(t + NA - 1, std::integral_constant<int, (S + NA - 1) % NA>{});
         static_for<0, 4>([&](auto sc) {
             constexpr int s = decltype(sc)::value;
             if constexpr (s < 3) read_x(std::integral_constant<int, s + 1>{});
@@ -168,25 +177,44 @@ gemm_i8_kernel(const GemmArgs p) {
             if constexpr (s == 3) issue_w(t + 2, par, I1{});
             __builtin_amdgcn_sched_barrier(0);
         });
-        wait_vmcnt<8>();
+        wait_vmcnt<IN_FLIGHT>();
         step_barrier();
     };
 
-    // Prologue: A(0) → stage 0, W(0) → raw[0], W(1) → raw[1]; A(0) and W(0) landed.
+    // Prologue: A(0) → stage 0, W(0) → raw[0], [A(1) → stage 1,] W(1) → raw[1]; A(0) and W(0) landed.
     issue_a(0, I0{});
     issue_w(0, I0{}, I0{});
     issue_w(0, I0{}, I1{});
+    if constexpr (NA == 3) issue_a(1, I1{});
     issue_w(1, I1{}, I0{});
     issue_w(1, I1{}, I1{});
-    wait_vmcnt<8>();
+    wait_vmcnt<IN_FLIGHT>();
     step_barrier();
 
+    using I2 = std::integral_constant<int, 2>;
     int t = 0;
-    for (; t + 1 < KT; t += 2) {
-        step(t, I0{});
-        step(t + 1, I1{});
+    if constexpr (NA == 2) {
+        for (; t + 1 < KT; t += 2) {
+            step(t, I0{}, I0{});
+            step(t + 1, I1{}, I1{});
+        }
+        if (t < KT) step(t, I0{}, I0{});
+    } else {
+        // (t mod 2, t mod 3) repeats every six steps.
+        for (; t + 5 < KT; t += 6) {
+            step(t, I0{}, I0{});
+            step(t + 1, I1{}, I1{});
+            step(t + 2, I0{}, I2{});
+            step(t + 3, I1{}, I0{});
+            step(t + 4, I0{}, I1{});
+            step(t + 5, I1{}, I2{});
+        }
+        if (t < KT) step(t, I0{}, I0{});
+        if (t + 1 < KT) step(t + 1, I1{}, I1{});
+        if (t + 2 < KT) step(t + 2, I0{}, I2{});
+        if (t + 3 < KT) step(t + 3, I1{}, I0{});
+        if (t + 4 < KT) step(t + 4, I0{}, I1{});
     }
-    if (t < KT) step(t, I0{});
 
     const bool has_bias = p.bias != nullptr;
     const int n_out = GLU ? p.glu_half : p.N;
@@ -230,7 +258,7 @@ gemm_i8_kernel(const GemmArgs p) {
     });
 }
 
-template <int BM, int NW, int WL, int EPI, int OUT>
+template <int BM, int NW, int WL, int EPI, int OUT, int NA>
 hipError_t launch_i8(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
@@ -239,14 +267,14 @@ hipError_t launch_i8(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = (slabs + NW - 1) / NW;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, NW, WL, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, NW, WL, EPI, OUT, NA>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int WL>
+template <int BM, int NW, int WL, int NA>
 hipError_t dispatch_i8(const GemmArgs &p, int epi, int out, hipStream_t stream) {
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_i8<BM, NW, WL, E, O>(p, stream);
+    if (epi == E && out == O) return launch_i8<BM, NW, WL, E, O, NA>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
