@@ -87,8 +87,9 @@ int sq8_create(int device, void *stream, sq8_ctx **out);
 /* Releases the context and its scratch memory. Replaces: the TensorGEMM instance's release. */
 int sq8_destroy(sq8_ctx *ctx);
 
-/* Changes the stream later launches go to. Replaces: the command queue passed at init
- * (TensorGEMM.swift:206). */
+/* Changes the stream later launches go to, after the work already queued on the previous stream has
+ * finished (the context's scratch and packing buffer serve one stream at a time).
+ * Replaces: the command queue passed at init (TensorGEMM.swift:206). */
 int sq8_set_stream(sq8_ctx *ctx, void *stream);
 
 /* 0 when `sq8_linear` runs this combination, else SQ8_EUNSUPPORTED / SQ8_EINVAL — the caller then

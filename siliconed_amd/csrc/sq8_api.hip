@@ -701,6 +701,13 @@ int sq8_destroy(sq8_ctx *ctx) {
 
 int sq8_set_stream(sq8_ctx *ctx, void *stream) {
     if (!ctx) return SQ8_EINVAL;
+    if (static_cast<hipStream_t>(stream) != ctx->stream) {
+        // The scratch and the packing buffer serve one stream at a time.
+        DeviceScope scope(ctx->device);
+        if (scope.error != hipSuccess) return hip_status(scope.error);
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
     ctx->stream = static_cast<hipStream_t>(stream);
     return SQ8_OK;
 }

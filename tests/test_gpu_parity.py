@@ -474,3 +474,30 @@ def test_tile_heights_same_bits(gemm, orc, monkeypatch, m, n, epi, out_dtype):
     monkeypatch.delenv("SQ8_TILE")
     assert bitwise_equal(outs["64"], outs["128"]) == 0 and bitwise_equal(outs["32"], outs["128"]) == 0
     judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
+
+
+def test_streams_switched_between_products(gemm, orc):
+    """Products on fp32 activations (each rounded into the context's scratch) on two streams in turn: the
+    switch waits for the work queued on the previous stream, so each product reads its own operand."""
+    m, k, n = 512, 1024, 768
+    x1, x2 = orc.normal_f32(3, (m, k)), orc.normal_f32(4, (m, k))
+    q = orc.uniform_i8(5, (n, k)).view(np.uint8)
+    s = orc.uniform_f32(6, (n,), 1e-3, 2e-2)
+    w = weight_tensor(q, False, "nk")
+    want1 = gemm.product(dev(x1), w, dev(s), layout="nk", out_dtype=torch.float32)
+    want2 = gemm.product(dev(x2), w, dev(s), layout="nk", out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    a1, a2 = dev(x1), dev(x2)
+    try:
+        for _ in range(3):
+            gemm.set_stream(s1)
+            with torch.cuda.stream(s1):
+                y1 = gemm.product(a1, w, dev(s), layout="nk", out_dtype=torch.float32)
+            gemm.set_stream(s2)
+            with torch.cuda.stream(s2):
+                y2 = gemm.product(a2, w, dev(s), layout="nk", out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            assert torch.equal(y1, want1) and torch.equal(y2, want2)
+    finally:
+        gemm.set_stream(torch.cuda.current_stream())
