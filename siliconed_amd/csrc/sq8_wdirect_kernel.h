@@ -167,6 +167,22 @@ __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_
     constexpr int CPR = 32 * ESZ / 16;
     constexpr int ROWS = 64 / CPR;
     constexpr int PER = 16 / ESZ;  // values per chunk
+    // The block's output tensor, head and column in it, once per block (wave-uniform): with the split
+    // and the head size multiples of 32 a 32-column block lies in one output and one head, and the
+    // 16-byte stores need no division per chunk.
+    const bool whole = p.split % 32 == 0 && p.head_dim % 32 == 0;
+    int which0 = 0, cc0 = col0, head0 = 0;
+    if (whole) {
+        if (p.split > 0) {
+            which0 = col0 / p.split;
+            cc0 = col0 - which0 * p.split;
+        }
+        if (p.head_dim > 0) {
+            head0 = cc0 / p.head_dim;
+            cc0 -= head0 * p.head_dim;
+        }
+    }
+    uint8_t *const base0 = kern::out_base(p, which0);
     static_for<0, 32 / ROWS>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         const int row = lane / CPR + ROWS * i, chunk = lane % CPR;
@@ -192,9 +208,15 @@ __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_
                             xr[e] = __fadd_rn(xr[e], __fmul_rn(p.gate ? p.gate[col + e] : 1.0f, __uint_as_float(v[e])));
                 }
             } else if (col + PER <= n_out && p.c_vec16) {
-                int which;
-                const int64_t off = out_index(p, m, col, which);
-                *reinterpret_cast<u32x4 *>(kern::out_base(p, which) + off * ESZ) = v;
+                if (whole) {
+                    const int cc = cc0 + chunk * PER;
+                    const int64_t off = p.head_dim > 0 ? ((int64_t)head0 * p.M + m) * p.head_dim + cc : (int64_t)m * p.ldc + cc;
+                    *reinterpret_cast<u32x4 *>(base0 + off * ESZ) = v;
+                } else {
+                    int which;
+                    const int64_t off = out_index(p, m, col, which);
+                    *reinterpret_cast<u32x4 *>(kern::out_base(p, which) + off * ESZ) = v;
+                }
             } else {
                 static_for<0, PER>([&](auto ec) {
                     constexpr int e = decltype(ec)::value;

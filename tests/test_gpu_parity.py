@@ -236,9 +236,10 @@ def test_fp32_activation_is_rounded_first(gemm, orc):
     assert torch.equal(a, r)
 
 
-@pytest.mark.parametrize("head_dim", [0, 128])
-def test_fused_qkv(gemm, orc, head_dim):
-    m, k, d = 300, 1024, 512
+@pytest.mark.parametrize("head_dim,d", [(0, 512), (128, 512), (48, 240), (0, 200), (40, 200)])
+def test_fused_qkv(gemm, orc, head_dim, d):
+    # d or head_dim not multiples of 32: a 32-column block straddles two outputs or two heads.
+    m, k = 300, 1024
     x, q, s, b = problem(orc, m, k, 3 * d, False, seed=31)
     w = weight_tensor(q, False, "nk")
     whole = gemm.product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), out_dtype=torch.bfloat16)
