@@ -38,7 +38,7 @@ RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a
 # 512 MiB copy), by (workload, weight layout), as measured by the rocprofv3 --pmc runs recorded in
 # profiles/gemm_wd_kernel_c1_up_int8_packed_gelu.md.
-TRAFFIC_BYTES = {("c1_up", "packed"): 541.6e6}
+TRAFFIC_BYTES = {("c1_up", "packed"): 543.4e6}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
 # name: M, K, N, weight type, epilogue, activation distribution, description.
