@@ -502,3 +502,50 @@ def test_streams_switched_between_products(gemm, orc):
             assert torch.equal(y1, want1) and torch.equal(y2, want2)
     finally:
         gemm.set_stream(torch.cuda.current_stream())
+
+
+@pytest.mark.parametrize("route", ["bf16", "fp32", "fp8w"])
+def test_non_finite_values_stay_in_their_rows_and_columns(gemm, orc, route):
+    """IEEE products as the reference's fp32 route computes them: a NaN in row r of A makes row r NaN,
+    +inf times positive codes +inf, times negative codes −inf, times a zero code NaN; an fp8 NaN code
+    (0x7F) makes its column NaN. Every other output keeps the bits of the same product without the
+    special values (rows and columns are independent)."""
+    m, k, n = 100, 256, 192
+    x = orc.normal_f32(50, (m, k))
+    fp8 = route == "fp8w"
+    _, q, s, b = problem(orc, m, k, n, fp8, 51)
+    q = q.copy()
+    if not fp8:
+        # The codes at k = 3 (q is [N, K]): 7 for outputs j < 5, −7 for 5 ≤ j < 10, 0 after.
+        q[:, 3] = 0
+        q[:5, 3] = np.uint8(7)
+        q[5:10, 3] = np.uint8(0xF9)
+    else:
+        q[17, 40] = 0x7F                         # a NaN code in output column 17
+    xs = x.copy()
+    xs[5, 7] = np.nan
+    xs[9, 3] = np.inf
+    w = weight_tensor(q, fp8, "nk")
+    kw = dict(layout="nk", bias=dev(b), out_dtype=torch.float32, rounding=route != "fp32")
+    if route == "fp32":
+        xa, xc = dev(xs), dev(x)
+    else:
+        xa, xc = bf16_dev(orc.f32_to_bf16(xs)), bf16_dev(orc.f32_to_bf16(x))
+    got = gemm.product(xa, w, dev(s), **kw).cpu().numpy()
+    clean = gemm.product(xc, w, dev(s), **kw).cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.isnan(got[5]).all()
+    if fp8:
+        assert np.isnan(got[:, 17]).all()
+        v = code_values(q, True)[:, 3]           # the codes +inf meets, per output column
+        live = np.arange(n) != 17
+        assert np.isposinf(got[9][live & (v > 0)]).all() and np.isneginf(got[9][live & (v < 0)]).all()
+        assert np.isnan(got[9][live & (v == 0)]).all()
+        keep = np.ones((m, n), bool)
+        keep[5] = keep[9] = False
+        keep[:, 17] = False
+    else:
+        assert np.isposinf(got[9, :5]).all() and np.isneginf(got[9, 5:10]).all() and np.isnan(got[9, 10:]).all()
+        keep = np.ones((m, n), bool)
+        keep[5] = keep[9] = False
+    assert np.array_equal(got[keep].view(np.uint32), clean[keep].view(np.uint32))
