@@ -260,9 +260,11 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     // [K, N] codes in place: repacked per product into the context's buffer when the repack runs near
     // the memory bandwidth (the reference's in-place route, Artifact.swift:443-459, at the speed of
     // the staged one: 37.7 MB of C1 codes cost ~12 µs against ~230 µs saved).
+    // The fp32 route and the residual epilogue run on the weight-direct kernels only: they repack any
+    // [K, N] weight (the general pack where the fast one does not apply).
     int wl_run = q.w_layout;
     if (q.w_layout == SQ8_KN && p.a_vec && k_steps &&
-        sq8::pack_is_fast(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue))) {
+        (q.exact || q.residual || sq8::pack_is_fast(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue)))) {
         const int64_t bytes = sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue));
         st = reserve_buffer(ctx, &ctx->wpack, &ctx->wpack_bytes, (size_t)bytes);
         if (st != SQ8_OK) return st;

@@ -149,7 +149,7 @@ class TensorGEMM:
                c: torch.Tensor, m: int, k: int, n: int, weight_offset: int = 0, scales_offset: int = 0,
                block: Optional[int] = None, rotation=None, rounding: bool = True, quantizing=None,
                prequantized=None, settled: bool = False, layout: str = "kn", bias: Optional[torch.Tensor] = None,
-               epilogue=None, fp8: Optional[bool] = None) -> float:
+               epilogue=None, fp8: Optional[bool] = None, columns: Optional[int] = None) -> float:
         """`linear(a:int8:weightOffset:scales:scalesOffset:perColumn:…:c:m:k:n:settled:)`
         (TensorGEMM.swift:264-290): C[m, n] = A[m, k] · (q · s), q `[k, n]` (`layout="kn"`, the
         map's) at `weight_offset` bytes into `int8`, its fp32 scales at `scales_offset` bytes into
@@ -173,7 +173,17 @@ class TensorGEMM:
 
         `block` = B: scales per block of B rows of K and column (GGUF Q8_0, fp32 `[k / B, n]` at
         `scales_offset`; `per_column` ignored), the product of sq8_linear_blocks.
+
+        `columns` ≤ n: only C's first `columns` columns are computed and written (the reference's
+        `submit(…columns:)`, TensorGEMM.swift:292-296); C keeps its row stride n. Not with block
+        scales, a quantization or a GLU epilogue.
         """
+        if columns is not None and columns != n:
+            if not 0 <= columns <= n:
+                raise ValueError(f"columns = {columns} outside [0, {n}]")
+            if block is not None or quantizing is not None or prequantized is not None or \
+                    epilogue in ("silu_glu", "situ_glu"):
+                raise abi.Unsupported(abi.EUNSUPPORTED, "columns with block scales, a quantization or a GLU epilogue")
         if block is not None:
             if rotation is not None or quantizing is not None or prequantized is not None or fp8:
                 raise abi.Unsupported(abi.EUNSUPPORTED, "block scales take int8 codes, no rotation, bf16 operands")
@@ -223,6 +233,10 @@ class TensorGEMM:
         if scales_offset % 4:
             raise ValueError("the scales' offset must be a multiple of 4 bytes")
         ldw = n if lay == abi.KN else k
+        ldc = n_out
+        if columns is not None and columns != n:
+            # The first `columns` of W's columns (its layout's stride kept) into C's first columns.
+            n = n_out = columns
         secs = ctypes.c_double(0.0)
         if exact:
             # The reference's `submit` on fp32 A: the fp32 route (three exact bf16 parts per value).
@@ -230,7 +244,7 @@ class TensorGEMM:
                                            ldw, _dev(scales, "scales") + scales_offset, abi.F32,
                                            abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR, 0,
                                            None if bias is None else _dev(bias, "bias"), epi,
-                                           _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                           _dev(c, "c"), _cdtype(c.dtype), ldc, m, k, n,
                                            None if settled else ctypes.byref(secs))
             abi.check(st, "sq8_linear_f32")
             return 0.0 if settled else secs.value
@@ -238,11 +252,22 @@ class TensorGEMM:
                 (_dev(int8, "int8") + weight_offset, wd, lay, ldw,
                  _dev(scales, "scales") + scales_offset, abi.SCALE_COLUMNS if per_column else abi.SCALE_TENSOR,
                  None if bias is None else _dev(bias, "bias"), epi,
-                 _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                 _dev(c, "c"), _cdtype(c.dtype), ldc, m, k, n,
                  None if settled else ctypes.byref(secs)))
         name = "sq8_linear_rotated" if group else "sq8_linear"
         abi.check(getattr(abi.load(), name)(*args), name)
         return 0.0 if settled else secs.value
+
+    def submit(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
+               c: torch.Tensor, m: int, k: int, n: int, columns: int, weight_offset: int = 0, scales_offset: int = 0,
+               rotation=None, rounding: bool = True, layout: str = "kn", bias: Optional[torch.Tensor] = None,
+               epilogue=None, fp8: Optional[bool] = None) -> None:
+        """`submit(a:int8:…:c:m:k:n:columns:)` (TensorGEMM.swift:292-360): the product on the first
+        `columns` of C only, queued and not waited for — the caller computes the other columns
+        meanwhile and synchronizes before reading C."""
+        self.linear(a, int8=int8, scales=scales, per_column=per_column, c=c, m=m, k=k, n=n,
+                    weight_offset=weight_offset, scales_offset=scales_offset, rotation=rotation, rounding=rounding,
+                    settled=True, layout=layout, bias=bias, epilogue=epilogue, fp8=fp8, columns=columns)
 
     def linear_bf16_weight(self, a: torch.Tensor, *, w: torch.Tensor, c: torch.Tensor, m: int, k: int, n: int,
                            weight_is_transposed: bool) -> float:

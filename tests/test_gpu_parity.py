@@ -549,3 +549,33 @@ def test_non_finite_values_stay_in_their_rows_and_columns(gemm, orc, route):
         keep = np.ones((m, n), bool)
         keep[5] = keep[9] = False
     assert np.array_equal(got[keep].view(np.uint32), clean[keep].view(np.uint32))
+
+
+@pytest.mark.parametrize("cols", [192, 200])
+@pytest.mark.parametrize("rounding,rotation", [(True, None), (False, None), (True, 64)])
+def test_submit_first_columns(gemm, orc, rounding, rotation, cols):
+    """`submit(…columns:)` (TensorGEMM.swift:292-360): the first `columns` of C computed and written, the
+    others untouched; queued, read after a sync. Whole 64-column slabs run the whole product's kernel:
+    the same bits as its first columns; a ragged count (200) runs the general kernel where the weight is
+    [K, N] and the fp32 route repacks it: within the bars of the truth."""
+    m, k, n = 130, 512, 320
+    x = orc.normal_f32(61, (m, k))
+    q = orc.uniform_i8(62, (k, n))                                    # [K, N], the map's layout
+    s = orc.uniform_f32(63, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(64, (n,), 0.0, 0.02)
+    a, w, sd, bd = dev(x), dev(q).view(torch.int8), dev(s), dev(b)
+    whole = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    gemm.linear(a, int8=w, scales=sd, per_column=True, c=whole, m=m, k=k, n=n, rotation=rotation, rounding=rounding,
+                bias=bd, epilogue="gelu_tanh")
+    part = torch.full((m, n), 7.0, dtype=torch.float32, device=DEV)
+    gemm.submit(a, int8=w, scales=sd, per_column=True, c=part, m=m, k=k, n=n, columns=cols, rotation=rotation,
+                rounding=rounding, bias=bd, epilogue="gelu_tanh")
+    gemm.synchronize()
+    assert (part[:, cols:] == 7.0).all()
+    if cols % 64 == 0:
+        assert torch.equal(part[:, :cols], whole[:, :cols])
+    truth_x = orc.rotate_groups(x, rotation) if rotation else x
+    if rounding:
+        truth_x = orc.f32_to_bf16(truth_x)
+    judge(orc, part[:, :cols].cpu().numpy(), truth_x, np.ascontiguousarray(q[:, :cols].T).view(np.uint8), False,
+          s[:cols], b[:cols], "gelu", torch.float32)
