@@ -55,6 +55,10 @@ def test_null_context_is_refused_not_crashed():
     assert lib.sq8_supports(None, 1, 3, 0, 1, 1, 0) == _abi.EINVAL
     assert lib.sq8_linear(None, None, 1, 0, None, 3, 0, 0, None, 1, None, 0, None, 1, 0, 0, 0, 0, None) == _abi.EINVAL
     assert lib.sq8_round_bf16(None, None, None, 0) == _abi.EINVAL
+    # The fp32 route and the bf16-weight product refuse a null context before touching anything.
+    assert lib.sq8_linear_f32(None, None, 64, 0, None, 3, 0, 64, None, 2, 1, 0, None, 0, None, 2, 64, 1, 64, 64,
+                              None) == _abi.EINVAL
+    assert lib.sq8_linear_bf16_weight(None, None, 2, 64, None, 0, 64, None, 64, 1, 64, 64, None) == _abi.EINVAL
     assert lib.sq8_create(0, None, None) == _abi.EINVAL
 
 
