@@ -1,0 +1,79 @@
+"""A seeded sweep of random shapes through the product's routes — bf16-rounded, fp32 (used whole), convrot
+(rounded or whole) and Q8_0 block scales — × layouts × epilogues × int8/fp8 × output types, each judged
+on sampled rows against the oracle's fp64 truth at the reference's bars (Diagnostic.swift:105-107,
+CapacityProbes.swift:541-553). Rows from 31 up: the per-channel metric averages over rows, and with a
+handful of rows a column whose exact values cancel makes it ill-conditioned (the products' error
+relative to Σ|x·w|·s stays at fp32's rounding there too)."""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import bf16_dev, dev, judge, problem, weight_tensor
+
+pytestmark = pytest.mark.gpu
+
+_NAMES = {"none": None, "gelu": "gelu_tanh", "silu": "silu_glu", "situ": "situ_glu"}
+
+
+def _case(i):
+    rng = random.Random(9000 + i)
+    route = rng.choice(["bf16", "bf16", "fp32", "rot", "q8"])
+    m = rng.choice([31, 64, 100, 257, 513, 1000])
+    n = rng.choice([64, 96, 130, 320, 1000, 2048])
+    layout = rng.choice(["nk", "kn", "packed"])
+    k = 64 * rng.randint(1, 40)
+    if route == "bf16" and layout != "packed" and rng.random() < 0.4:
+        k = rng.randint(8, 700)                    # ragged K: the general kernel
+    epi = rng.choice(["none", "gelu", "silu", "situ"] if route != "q8" else ["none", "gelu", "silu"])
+    if epi in ("silu", "situ") and n % 2:
+        n += 1
+    fp8 = route in ("bf16", "fp32") and rng.random() < 0.3
+    out = rng.choice([torch.float32, torch.bfloat16])
+    grp = rng.choice([g for g in (4, 16, 64, 256) if k % g == 0]) if route == "rot" else 0
+    rounding = rng.random() < 0.5
+    return route, m, k, n, layout, epi, fp8, out, grp, rounding
+
+
+@pytest.mark.parametrize("i", range(60))
+def test_random_shape(gemm, orc, i):
+    route, m, k, n, layout, epi, fp8, out, grp, rounding = _case(i)
+    rows = orc.sample_rows(m, 48)
+    if route == "q8":
+        x = orc.normal_bf16(i, (m, k))
+        q = orc.uniform_i8(i + 1, (n, k))
+        d = orc.uniform_f32(i + 2, (n, k // 32), 1e-3, 2e-2).astype(np.float16)
+        b = orc.normal_f32(i + 3, (n,), 0.0, 0.02)
+        if layout == "packed":
+            w, s, lay = gemm.pack_blocks(dev(q).view(torch.int8), dev(d.astype(np.float32)), 32, layout="nk",
+                                         glu=epi in ("silu", "situ")), None, "nk"
+        elif layout == "kn":
+            w, s, lay = (dev(np.ascontiguousarray(q.T)).view(torch.int8),
+                         dev(np.ascontiguousarray(d.T).astype(np.float32)), "kn")
+        else:
+            w, s, lay = dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16), "nk"
+        y = gemm.product_blocks(bf16_dev(x), w, s, 32, layout=lay, bias=dev(b), epilogue=_NAMES[epi], out_dtype=out)
+        torch.cuda.synchronize()
+        wv = q.astype(np.float32) * np.repeat(d.astype(np.float32), 32, axis=1)
+        judge(orc, y.float().cpu().numpy(), x, wv, None, np.ones(n, np.float32), b, epi, out, rows=rows, values=True)
+        return
+    x32 = orc.normal_f32(i, (m, k))
+    _, q, s, b = problem(orc, m, k, n, fp8, i + 1)
+    w = weight_tensor(q, fp8, "nk" if layout == "nk" else "kn")
+    if layout == "packed":
+        w = gemm.pack(w, layout="kn", glu=epi in ("silu", "situ"), fp8=fp8 or None)
+    lay = "nk" if layout == "nk" else "kn"
+    kw = dict(layout=lay, bias=dev(b), epilogue=_NAMES[epi], out_dtype=out)
+    if route == "rot":
+        y = gemm.product(dev(x32), w, dev(s), rotation=grp, rounding=rounding, **kw)
+        xr = orc.rotate_groups(x32, grp)
+        truth_x = orc.f32_to_bf16(xr) if rounding else xr
+    elif route == "fp32":
+        y = gemm.product(dev(x32), w, dev(s), rounding=False, **kw)
+        truth_x = x32
+    else:
+        truth_x = orc.f32_to_bf16(x32)
+        y = gemm.product(bf16_dev(truth_x), w, dev(s), **kw)
+    torch.cuda.synchronize()
+    judge(orc, y.float().cpu().numpy(), truth_x, q, fp8, s, b, epi, out, rows=rows)
