@@ -77,3 +77,34 @@ def test_random_shape(gemm, orc, i):
         y = gemm.product(bf16_dev(truth_x), w, dev(s), **kw)
     torch.cuda.synchronize()
     judge(orc, y.float().cpu().numpy(), truth_x, q, fp8, s, b, epi, out, rows=rows)
+
+
+def _w8a8_case(i):
+    rng = random.Random(7000 + i)
+    m = rng.choice([1, 2, 7, 31, 100, 257, 1000])
+    layout = rng.choice(["nk", "kn", "packed"])
+    k = 64 * rng.randint(1, 48) if layout == "packed" else rng.randint(8, 3000)
+    n = rng.choice([8, 64, 130, 320, 1000, 2048])
+    groups = [g for g in (0, 4, 16, 64, 256) if g == 0 or k % g == 0]
+    return m, k, n, layout, rng.choice(groups), rng.random() < 0.7
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_shape_w8a8_at_the_bit(gemm, orc, i):
+    """The W8A8 route on random shapes, one row up: the same bits as the oracle's recipe (codes and row
+    scales of W8A8.quantize, the integer sums exact, float(Σ) · (s_x · s_w))."""
+    m, k, n, layout, g, per_col = _w8a8_case(i)
+    x = orc.normal_f32(500 + i, (m, k))
+    q = orc.uniform_i8(501 + i, (n, k))
+    sw = orc.uniform_f32(502 + i, (n if per_col else 1,), 1e-3, 2e-2)
+    codes, sx = orc.quantize_rows(x, g)
+    expected = orc.w8a8_product(codes, sx, q, False, sw)
+    if layout == "packed":
+        w, lay = gemm.pack(dev(q).view(torch.int8), layout="nk"), "nk"
+    elif layout == "kn":
+        w, lay = dev(np.ascontiguousarray(q.T)).view(torch.int8), "kn"
+    else:
+        w, lay = dev(q).view(torch.int8), "nk"
+    got = gemm.product_quantized(dev(x), w, dev(sw), group=g, layout=lay, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), expected.view(np.uint32))
