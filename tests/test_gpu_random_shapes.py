@@ -108,3 +108,41 @@ def test_random_shape_w8a8_at_the_bit(gemm, orc, i):
     got = gemm.product_quantized(dev(x), w, dev(sw), group=g, layout=lay, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy().view(np.uint32), expected.view(np.uint32))
+
+
+def _exact_case(i):
+    rng = random.Random(5000 + i)
+    m = rng.choice([1, 2, 3, 7, 16, 33, 130, 600])
+    layout = rng.choice(["nk", "kn", "packed"])
+    route = rng.choice(["bf16", "fp32"])
+    # Ragged K (the general kernel) on the rounded route; the fp32 route takes whole steps of 64.
+    k = 64 * rng.randint(1, 60) if layout == "packed" or route == "fp32" or rng.random() < 0.6 else rng.randint(8, 2000)
+    n = rng.choice([8, 64, 96, 130, 320, 1000, 3072])
+    return m, k, n, layout, route, rng.choice([torch.float32, torch.bfloat16])
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_shape_exact_sums_at_the_bit(gemm, orc, i):
+    """Integer activations in [−5, 5] and codes: every product and every fp32 sum exact in any order
+    (|Σ| ≤ 5·127·K < 2^24), so from one row up, on whichever kernel the shape takes (skinny, short or
+    main tiles, the general kernel for ragged K), the output is the reference's two roundings bit for bit:
+    the scale after the sum (TensorGEMM.swift:175-179), then the bias (Ops.swift:400-407)."""
+    m, k, n, layout, route, out = _exact_case(i)
+    rng = np.random.default_rng(4000 + i)
+    xi = rng.integers(-5, 6, (m, k)).astype(np.float32)
+    q = orc.uniform_i8(4100 + i, (n, k)).view(np.uint8)
+    s = orc.uniform_f32(4200 + i, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(4300 + i, (n,), 0.0, 0.02)
+    w = weight_tensor(q, False, "nk" if layout == "nk" else "kn")
+    if layout == "packed":
+        w = gemm.pack(w, layout="kn")
+    lay = "nk" if layout == "nk" else "kn"
+    x = dev(xi) if route == "fp32" else bf16_dev(orc.f32_to_bf16(xi))
+    y = gemm.product(x, w, dev(s), layout=lay, bias=dev(b), out_dtype=out, rounding=route != "fp32")
+    torch.cuda.synchronize()
+    total = (xi.astype(np.float64) @ q.view(np.int8).astype(np.float64).T).astype(np.float32)   # exact
+    want = (total * s[None, :]).astype(np.float32) + b[None, :]
+    if out == torch.float32:
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32))
+    else:
+        assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), orc.f32_to_bf16(want.astype(np.float32)))
