@@ -146,3 +146,36 @@ def test_random_shape_exact_sums_at_the_bit(gemm, orc, i):
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32))
     else:
         assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), orc.f32_to_bf16(want.astype(np.float32)))
+
+
+@pytest.mark.parametrize("i", range(20))
+def test_random_shape_block_scales_at_the_bit(gemm, orc, i):
+    """GGUF Q8_0 block scales on integer activations: each block's sum Σ a·q is exact, so the product's
+    arithmetic is fixed — per block of 32, in K order, acc = fl(P·d + acc) (one fused rounding), then
+    the bias — and restated in numpy (float64 holds P·d + acc exactly) it gives the same bits, from one
+    row up, on every layout."""
+    rng = random.Random(3000 + i)
+    m = rng.choice([1, 2, 5, 33, 130, 600])
+    k = 64 * rng.randint(1, 40)
+    n = rng.choice([8, 64, 130, 320, 1000])
+    layout = rng.choice(["nk", "kn", "packed"])
+    r = np.random.default_rng(3100 + i)
+    xi = r.integers(-5, 6, (m, k)).astype(np.float32)
+    q = orc.uniform_i8(3200 + i, (n, k))
+    d = orc.uniform_f32(3300 + i, (n, k // 32), 1e-3, 2e-2).astype(np.float16)
+    b = orc.normal_f32(3400 + i, (n,), 0.0, 0.02)
+    if layout == "packed":
+        w, s, lay = gemm.pack_blocks(dev(q).view(torch.int8), dev(d.astype(np.float32)), 32, layout="nk"), None, "nk"
+    elif layout == "kn":
+        w, s, lay = dev(np.ascontiguousarray(q.T)).view(torch.int8), dev(np.ascontiguousarray(d.T).astype(np.float32)), "kn"
+    else:
+        w, s, lay = dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16), "nk"
+    y = gemm.product_blocks(bf16_dev(orc.f32_to_bf16(xi)), w, s, 32, layout=lay, bias=dev(b), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    acc = np.zeros((m, n), np.float32)
+    qf = q.astype(np.float64)
+    for blk in range(k // 32):
+        p = xi[:, 32 * blk:32 * blk + 32].astype(np.float64) @ qf[:, 32 * blk:32 * blk + 32].T     # exact
+        acc = (p * d[:, blk].astype(np.float64)[None, :] + acc.astype(np.float64)).astype(np.float32)
+    want = (acc + b[None, :]).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
