@@ -179,3 +179,31 @@ def test_random_shape_block_scales_at_the_bit(gemm, orc, i):
         acc = (p * d[:, blk].astype(np.float64)[None, :] + acc.astype(np.float64)).astype(np.float32)
     want = (acc + b[None, :]).astype(np.float32)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_shape_fp8_exact_sums_at_the_bit(gemm, orc, i):
+    """fp8-e4m3 codes of values in [−1, 1] (multiples of 2^−9) times integer activations in [−5, 5]:
+    every partial sum is a multiple of 2^−9 below 2^15, exact in fp32 in any order (K ≤ 6400), so the
+    output is the reference's two roundings bit for bit, from one row up, on every layout."""
+    rng = random.Random(6000 + i)
+    m = rng.choice([1, 3, 17, 64, 300])
+    k = 64 * rng.randint(1, 50)
+    n = rng.choice([8, 64, 130, 1000])
+    layout = rng.choice(["nk", "kn", "packed"])
+    r = np.random.default_rng(6100 + i)
+    xi = r.integers(-5, 6, (m, k)).astype(np.float32)
+    q = orc.f32_to_e4m3(r.uniform(-1.0, 1.0, (n, k)).astype(np.float32))       # [N, K] codes
+    from refgen import code_values
+    wv = code_values(q, True).astype(np.float64)
+    s = orc.uniform_f32(6200 + i, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(6300 + i, (n,), 0.0, 0.02)
+    w = weight_tensor(q, True, "nk" if layout == "nk" else "kn")
+    if layout == "packed":
+        w = gemm.pack(w, layout="kn", fp8=True)
+    y = gemm.product(bf16_dev(orc.f32_to_bf16(xi)), w, dev(s), layout="nk" if layout == "nk" else "kn", bias=dev(b),
+                     out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    total = (xi.astype(np.float64) @ wv.T).astype(np.float32)                     # exact
+    want = (total * s[None, :]).astype(np.float32) + b[None, :]
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32))
