@@ -204,41 +204,85 @@ def derived_peak(cus: int) -> dict:
     return out
 
 
+def settle(step, settle_ms: float) -> dict:
+    """The clock-settle phase: `step` launched back to back until `settle_ms` of wall time has passed
+    (synchronizing every few launches so the time is the GPU's). The shader clock of this chip ramps
+    over the first tens of milliseconds of sustained MFMA work and the power limit then sets it; a
+    measurement that starts cold times the ramp. Returns what ran."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    launches = 0
+    while True:
+        for _ in range(8):
+            step()
+        launches += 8
+        torch.cuda.synchronize()
+        if 1e3 * (time.perf_counter() - t0) >= settle_ms:
+            break
+    return {"settle_ms": round(1e3 * (time.perf_counter() - t0), 1), "settle_launches": launches}
+
+
+def launch_stats(times_ms) -> dict:
+    """Per-launch statistics of the timed steps (each bracketed by its own HIP events)."""
+    t = sorted(times_ms)
+    return {"min": round(t[0], 5), "median": round(float(np.median(t)), 5), "max": round(t[-1], 5)}
+
+
+def c4_measure(route: str, steps: int, warmup: int, settle_ms: float) -> dict:
+    """One synthetic single-stream DiT block forward (siliconed_amd.dit_block) on `route` ("bf16", or
+    "w8a8" with convrot 256): hidden 3072, 24 heads of 128, 4096 image + 512 text tokens. Each timed
+    forward is bracketed by its own HIP events; returns the mean, min and median ms."""
+    import torch
+    from siliconed_amd.dit_block import DiTBlock
+    S, d, heads = 4096 + 512, 3072, 24
+    w8a8 = route == "w8a8"
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=SEEDS["w"], route=route, group=256 if w8a8 else 0)
+    x = torch.from_numpy(normal_f32(SEEDS["x"], S * d).reshape(S, d)).cuda()
+    temb = torch.from_numpy(normal_f32(SEEDS["bias"], d)).cuda()
+    # The block updates its residual stream in place (as the reference's stream buffer): each step
+    # gets its own copy of x, made before the timed region; the settle and warm-up forwards reuse one.
+    streams = [x.clone() for _ in range(steps)]
+    work = x.clone()
+    st = settle(lambda: blk.forward_(work, temb), settle_ms)
+    for _ in range(warmup):
+        blk.forward_(work, temb)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    ev[0].record()
+    for i in range(steps):
+        blk.forward_(streams[i], temb)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    ms = ev[0].elapsed_time(ev[steps]) / steps
+    flops = blk.flops(S)
+    out = {"ms": round(ms, 4), "per_forward_ms": launch_stats(per), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+           "flops": flops, "steps": steps, "warmup": warmup, "wall_ms_per_step": round(1e3 * wall / steps, 4), **st}
+    del blk, streams, work, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def dit_block(args) -> int:
     """C4: one synthetic single-stream DiT block forward (siliconed_amd.dit_block): hidden 3072, 24
     heads of 128, 4096 image + 512 text tokens, int8 per-channel modulation / QKV / out / MLP-4×
     weights, bf16 attention, fp32 residual. value: the block's forward time in ms (HIP events over the
     timed forwards); `tflops` beside it (linear + attention FLOPs over that time)."""
-    import torch
-    from siliconed_amd.dit_block import DiTBlock
     S, d, heads = 4096 + 512, 3072, 24
     w8a8 = args.workload == "c4_block_w8a8"
-    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=SEEDS["w"], route="w8a8" if w8a8 else "bf16", group=256 if w8a8 else 0)
-    x = torch.from_numpy(normal_f32(SEEDS["x"], S * d).reshape(S, d)).cuda()
-    temb = torch.from_numpy(normal_f32(SEEDS["bias"], d)).cuda()
-    steps = max(args.steps // 5, 5)
-    # The block updates its residual stream in place (as the reference's stream buffer): each step
-    # gets its own copy of x, made before the timed region.
-    streams = [x.clone() for _ in range(steps)]
-    for _ in range(max(args.warmup // 20, 5)):
-        blk.forward(x, temb)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for i in range(steps):
-        blk.forward_(streams[i], temb)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = ev0.elapsed_time(ev1) / steps
-    flops = blk.flops(S)
-    tflops = flops / (ms * 1e-3) / 1e12
+    steps = max(args.steps // 2, 5)
+    warm = max(args.warmup // 20, 2)
+    r = c4_measure("w8a8" if w8a8 else "bf16", steps, warm, args.settle_ms)
+    ms, flops, tflops = r["ms"], r["flops"], r["tflops"]
     result = {
         "metric": ("DiT block forward ms (hidden 3072, 24x128 heads, 4608 tokens, int8 weights"
                    + (", W8A8 route, convrot 256" if w8a8 else "") + ") on 1 MI355X"),
         "value": round(ms, 4), "unit": "ms", "tflops": round(tflops, 2), "n_gpus": 1, "steps": steps,
-        "warmup": max(args.warmup // 20, 5), "ms_per_step": round(1e3 * wall / steps, 4), "higher_is_better": False,
+        "warmup": warm, "settle_ms": r["settle_ms"], "per_forward_ms": r["per_forward_ms"],
+        "ms_per_step": r["wall_ms_per_step"], "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if w8a8 else "bf16",
         "data": f"synthetic, seeded: x, temb SplitMix64 + Box-Muller; weights torch generator seed {SEEDS['w']}",
         "config": {"workload": f"{args.workload}: one single-stream DiT block (modulation, modulated RMSNorm, fused QKV, "
@@ -257,9 +301,14 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # The clocks reach their steady state only after ~50 ms of sustained work: 10 warm-up steps leave
-    # the first timed steps 30 % slow (0.36 ms against 0.27 ms each on the default workload).
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    # The clocks reach their steady state only after ~50 ms of sustained work: a short warm-up counted
+    # in steps leaves the first timed steps ~30 % slow (0.36 ms against 0.27 ms each on the default
+    # workload). The settle phase runs the same step for a fixed time before the counted warm-up.
+    ap.add_argument("--settle-ms", type=float, default=400.0,
+                    help="wall time of back-to-back steps before the counted warm-up (clock settle)")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="default workload only: skip the C4 block forwards reported beside the line")
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4_block", "c4_block_w8a8"], default="c1_up")
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once by sq8_pack_weight")
@@ -374,29 +423,35 @@ def main() -> int:
         def step():
             ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
 
+    settled = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # Every timed step is bracketed by HIP events on torch's current stream, the stream the context
+    # launches on: ev[i] before step i, ev[steps] after the last (rotated workloads: three marks a step,
+    # around the activation pass and the product).
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)] if group else None
     t0 = time.perf_counter()
-    ev0.record()
+    ev[0].record()
     for i in range(args.steps):
         if group:
             step(marks[i])
         else:
             step()
-    ev1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # The events are recorded on torch's current stream, the stream the context launches on.
-    step_ms = ev0.elapsed_time(ev1) / args.steps
+    step_ms = ev[0].elapsed_time(ev[args.steps]) / args.steps
+    per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
     kernel_ms = step_ms
+    per_kernel = per_step
     rotation = None
     if group:
         # The product kernel's own time (the roofline's), and the rotation pass's, from the marks
         # around each launch; the step (value) is both.
-        kernel_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
+        per_kernel = [m[1].elapsed_time(m[2]) for m in marks]
+        kernel_ms = sum(per_kernel) / args.steps
         rot_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
         rot_bytes = 4 * M * K + (1 if args.workload in W8A8 else 2) * M * K
         rotation = {"kind": "rotate + quantize to int8" if args.workload in W8A8 else "rotate + round to bf16",
@@ -453,11 +508,22 @@ def main() -> int:
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         **({"pct_int8_peak": round(100.0 * tflops / PEAK_INT8_TOPS, 2)} if w8a8 else {}),
         "kernel_ms": round(kernel_ms, 5),
+        "kernel_ms_per_launch": launch_stats(per_kernel),
+        **settled,
         "roofline": roofline,
         **({"activation_pass": rotation} if rotation else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "peak_derived": derived_peak(props.multi_processor_count)},
     }
+    if args.workload == "c1_up" and not args.no_c4:
+        # C4 (a full DiT block forward, both product routes) beside the headline, so that the default
+        # line records it; each route settles its clock first.
+        del wd, xd, out
+        torch.cuda.empty_cache()
+        for route in ("bf16", "w8a8"):
+            r = c4_measure(route, steps=10, warmup=2, settle_ms=min(args.settle_ms, 300.0))
+            result[f"c4_block_{route}_ms"] = r["ms"]
+            result[f"c4_block_{route}"] = {k: r[k] for k in ("per_forward_ms", "tflops", "steps", "settle_ms")}
     if not args.no_cpu:
         xb = x.view(torch.int16).numpy()
         result["cpu_baseline"] = cpu_baseline(args.workload, xb, q.view(torch.uint8).numpy() if fp8 else q, s, b,

@@ -320,9 +320,14 @@ void orc_w8a8_product(const int8_t *codes, int64_t ldq, const float *sx, const i
 /* ---------------------------------------------------------------------------------------------
  * Epilogues in double.
  * ------------------------------------------------------------------------------------------- */
+/* GELU-tanh, ½x(1 + tanh u) with u = √(2/π)(x + 0.044715x³) (QwenImage21.swift:953-963, the double
+ * form rounded once), evaluated as x / (1 + e^(−2u)): the identical function, since ½(1 + tanh u) =
+ * 1 / (1 + e^(−2u)), without the cancellation of 1 + tanh u in the negative tail, where the literal form
+ * returns −0 for x ≤ −8 although the value (about x·e^(2u), −3·10⁻²¹ at x = −8) is a normal fp32. */
 double orc_gelu_tanh(double x) {
     const double c = sqrt(2.0 / M_PI);
-    return 0.5 * x * (1.0 + tanh(c * (x + 0.044715 * x * x * x)));
+    const double u = c * (x + 0.044715 * x * x * x);
+    return x / (1.0 + exp(-2.0 * u));
 }
 
 double orc_silu_glu(double gate, double up) { return gate / (1.0 + exp(-gate)) * up; }

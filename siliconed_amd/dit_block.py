@@ -39,21 +39,6 @@ def quantize_int8(w: torch.Tensor):
     return q, s.float()
 
 
-def rms_modulate(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
-                 to_bf16: bool = True) -> torch.Tensor:
-    """RMS(x)·w·(1 + scale) + shift, fp32 arithmetic; rounded to bf16 (the next product's operand on
-    the bf16 route) unless `to_bf16` is false (the W8A8 route quantizes the fp32 row)."""
-    r = torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + EPS)
-    y = (x * r) * w * (1.0 + scale) + shift
-    return y.to(torch.bfloat16) if to_bf16 else y
-
-
-def rms_heads(t: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """Per-head RMSNorm of q or k, [heads, S, head_dim] bf16, fp32 arithmetic."""
-    t32 = t.float()
-    return (t32 * torch.rsqrt(t32.pow(2).mean(dim=-1, keepdim=True) + EPS) * w).to(torch.bfloat16)
-
-
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Softmax attention of [heads, S, head_dim] bf16, no mask, on torch's fused kernels only."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -77,10 +62,9 @@ class DiTBlock:
         g = torch.Generator(device=dev).manual_seed(seed)
 
         def linear(n_out: int, k: int):
-            w = torch.randn((n_out, k), device=dev, generator=g) * 0.02
-            q, s = quantize_int8(w)
+            q, s = quantize_int8(torch.randn((n_out, k), device=dev, generator=g) * 0.02)
             b = torch.randn(n_out, device=dev, generator=g) * 0.02
-            return {"w": w, "q": q, "s": s, "b": b, "packed": self.ctx.pack(q, layout="nk")}
+            return {"q": q, "s": s, "b": b, "packed": self.ctx.pack(q, layout="nk")}
 
         self.mod = linear(6 * d, d)
         self.qkv = linear(3 * d, d)
@@ -145,48 +129,6 @@ class DiTBlock:
     def forward(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
         """x fp32 [S, d] (the residual stream), temb [d]: the block's output, fp32 [S, d] (x kept)."""
         return self.forward_(x.clone(), temb)
-
-    def _rotate(self, a: torch.Tensor) -> torch.Tensor:
-        """a·R by groups of `group` in fp32 (R = H/√G, H the Kronecker power of the regular H4)."""
-        g = self.group
-        if not g:
-            return a
-        h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float32, device=a.device)
-        h = torch.ones((1, 1), device=a.device)
-        while h.shape[0] < g:
-            h = torch.kron(h, h4)
-        return (a.reshape(a.shape[0], -1, g) @ (h / g ** 0.5)).reshape(a.shape)
-
-    def _quantized(self, a: torch.Tensor) -> torch.Tensor:
-        """The W8A8 operand in fp32: a rotated, quantized per row (s = max|y|/127, rint) and scaled back."""
-        y = self._rotate(a.float())
-        s = (y.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(1e-30)
-        return torch.round(y / s).clamp(-128, 127) * s
-
-    def reference(self, x: torch.Tensor, temb: torch.Tensor) -> torch.Tensor:
-        """The same block in fp32 with the dequantised weights (Float(q)·s) and fp32 math attention:
-        the check of `forward` (operands rounded to bf16 where `forward` rounds them; on the W8A8
-        route quantized per row after the rotation, as `forward` quantizes them — the product of a
-        rotated operand with the stored weight is the product with the convrot weight (q·s)·R)."""
-        def lin(a, L, act=None, w8=None):
-            w8 = self.route == "w8a8" if w8 is None else w8
-            a = self._quantized(a) if w8 else a.float()
-            y = a @ (L["q"].float() * L["s"][:, None]).t() + L["b"]
-            return torch.nn.functional.gelu(y, approximate="tanh") if act else y
-        S, d = x.shape
-        mod = lin(temb.to(torch.bfloat16)[None], self.mod, w8=False)[0]
-        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod.chunk(6)
-        w8 = self.route == "w8a8"
-        n = rms_modulate(x, self.norm_a, scale_a, shift_a, to_bf16=not w8)
-        qkv = lin(n, self.qkv).to(torch.bfloat16).view(S, 3, self.heads, self.hd).permute(1, 2, 0, 3)
-        q, k, v = (rms_heads(t.contiguous(), w).float() if w is not None else t.float()
-                   for t, w in zip(qkv, (self.norm_q, self.norm_k, None)))
-        att = torch.softmax((q @ k.transpose(1, 2).contiguous()) / self.hd ** 0.5, dim=-1) @ v
-        o = att.to(torch.bfloat16).transpose(0, 1).reshape(S, d)
-        x = x + gate_a * lin(o, self.out)
-        m = rms_modulate(x, self.norm_f, scale_f, shift_f, to_bf16=not w8)
-        h = lin(m, self.up, act=True).to(torch.bfloat16)
-        return x + gate_f * lin(h, self.down)
 
     def flops(self, S: int) -> float:
         """Linear FLOPs (modulation included) + attention's two products."""

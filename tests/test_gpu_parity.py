@@ -266,16 +266,23 @@ def test_empty_and_refused(gemm):
 
 # ---- the baseline's shapes, on sampled rows ----------------------------------------------------
 
-@pytest.mark.parametrize("case", ["c1_up_gelu", "c1_down", "c2_qkv", "c2_text", "c3_gate_up_fp8", "c3_down_fp8"])
+BASELINE_CASES = {
+    "c0": (1024, 3072, 3072, False, "none"),             # configs[0] at its full M (64-row tiles)
+    "c1_up_gelu": (4096, 3072, 12288, False, "gelu"),
+    "c1_down": (4096, 12288, 3072, False, "none"),
+    "c2_qkv": (4608, 3072, 9216, False, "none"),
+    "c2_text": (512, 3072, 3072, False, "none"),
+    "c3_gate_up_fp8": (4096, 3840, 20480, True, "silu"),
+    "c3_down_fp8": (4096, 10240, 3840, True, "none"),
+    "c3_plain_fp8": (4096, 3840, 12288, True, "none"),   # the plain fp8 W [12288, 3840] of configs[3]
+}
+
+
+@pytest.mark.parametrize("case", ["c0", "c1_up_gelu", "c1_down", "c2_qkv", "c2_text", "c3_gate_up_fp8", "c3_down_fp8",
+                                  "c3_plain_fp8"])
 def test_baseline_shapes_sampled_rows(gemm, orc, case):
-    m, k, n, fp8, epi = {
-        "c1_up_gelu": (4096, 3072, 12288, False, "gelu"),
-        "c1_down": (4096, 12288, 3072, False, "none"),
-        "c2_qkv": (4608, 3072, 9216, False, "none"),
-        "c2_text": (512, 3072, 3072, False, "none"),
-        "c3_gate_up_fp8": (4096, 3840, 20480, True, "silu"),
-        "c3_down_fp8": (4096, 10240, 3840, True, "none"),
-    }[case]
+    m, k, n, fp8, epi = BASELINE_CASES[case]
+    print(f"baseline shape {case}: {m}x{k}x{n} fp8={fp8} epilogue {epi}", flush=True)
     x, q, s, b = problem(orc, m, k, n, fp8, seed=1000 + k)
     for layout in ("kn", "nk"):
         got = run(gemm, x, q, s, b, fp8, layout, epi, torch.bfloat16)
@@ -330,14 +337,12 @@ def test_packed_glu_weight_refuses_plain_epilogue(gemm, orc):
     assert abi.load().sq8_packed_bytes(64, 3, 1) == -1
 
 
-@pytest.mark.parametrize("case", ["c1_up_gelu", "c1_down", "c2_qkv", "c3_gate_up_fp8"])
+@pytest.mark.parametrize("case", ["c0", "c1_up_gelu", "c1_down", "c2_qkv", "c2_text", "c3_gate_up_fp8", "c3_down_fp8",
+                                  "c3_plain_fp8"])
 def test_packed_baseline_shapes(gemm, orc, case):
-    m, k, n, fp8, epi = {
-        "c1_up_gelu": (4096, 3072, 12288, False, "gelu"),
-        "c1_down": (4096, 12288, 3072, False, "none"),
-        "c2_qkv": (4608, 3072, 9216, False, "none"),
-        "c3_gate_up_fp8": (4096, 3840, 20480, True, "silu"),
-    }[case]
+    # The staged (packed) weight, as bench.py runs every workload.
+    m, k, n, fp8, epi = BASELINE_CASES[case]
+    print(f"packed baseline shape {case}: {m}x{k}x{n} fp8={fp8} epilogue {epi}", flush=True)
     x, q, s, b = problem(orc, m, k, n, fp8, seed=2000 + k)
     pk = gemm.pack(weight_tensor(q, fp8, "kn"), layout="kn", glu=epi == "silu", fp8=fp8 or None)
     name = {"gelu": "gelu_tanh", "silu": "silu_glu", "none": None}[epi]

@@ -183,7 +183,10 @@ def test_exact_rows_match_float64_products(orc):
         y = orc.exact_rows(rows, a, np.ascontiguousarray(q.T).astype(np.float32), True, k, n, scale=s, bias=b)
         assert np.array_equal(y, d[f"y_none_{i}"])
         g = orc.exact_rows(rows, a, q.astype(np.float32), False, k, n, scale=s, bias=b, epilogue=orc.EPI_GELU_TANH)
-        np.testing.assert_allclose(g, d[f"y_gelu_{i}"], rtol=1e-14, atol=1e-300)
+        # The fixture is torch's float64 ½x(1 + tanh u), whose 1 + tanh u cancels for negative x: its own
+        # error there is a few units of 2⁻⁵³ times ½|x|, which bounds the difference beside 1e-14 relative.
+        pre = d[f"y_none_{i}"]
+        assert np.all(np.abs(g - d[f"y_gelu_{i}"]) <= 1e-14 * np.abs(d[f"y_gelu_{i}"]) + 4 * 2.0 ** -53 * 0.5 * np.abs(pre))
         h = orc.exact_rows(rows, a, q.astype(np.float32), False, k, n, scale=s, bias=b, epilogue=orc.EPI_SILU_GLU)
         np.testing.assert_allclose(h, d[f"y_silu_glu_{i}"], rtol=1e-14, atol=1e-300)
 
@@ -269,12 +272,45 @@ def test_situ_closed_forms(orc):
     assert math.isclose(f(1.0, 1.0), 4 * math.tanh(0.25) / (1 + math.exp(-1)) * 25 * math.tanh(0.04), rel_tol=1e-15)
 
 
+def _gelu_tanh_decimal(x: float) -> float:
+    """½x(1 + tanh u), u = √(2/π)(x + 0.044715x³), the reference's formula evaluated in 420-digit
+    decimal arithmetic (tanh u = (e^(2u) − 1)/(e^(2u) + 1)): 1 + tanh u keeps more than 60 digits down
+    to e^(2u) = 10⁻³⁵⁰, past double's range."""
+    import decimal
+    with decimal.localcontext() as c:
+        c.prec = 420
+        pi = decimal.Decimal("3.14159265358979323846264338327950288419716939937510582097494")
+        d = decimal.Decimal(x)
+        u = (decimal.Decimal(2) / pi).sqrt() * (d + decimal.Decimal("0.044715") * d * d * d)
+        e = (2 * u).exp()
+        return float(decimal.Decimal("0.5") * d * (1 + (e - 1) / (e + 1)))
+
+
 def test_activations_match_torch_float64(orc):
     x = torch.linspace(-12, 12, 4001, dtype=torch.float64)
     g = np.array([orc.lib().orc_gelu_tanh(float(v)) for v in x])
     np.testing.assert_allclose(g, torch.nn.functional.gelu(x, approximate="tanh").numpy(), rtol=1e-13, atol=1e-15)
     s = np.array([orc.lib().orc_silu_glu(float(v), 1.5) for v in x])
     np.testing.assert_allclose(s, (torch.nn.functional.silu(x) * 1.5).numpy(), rtol=1e-13, atol=1e-15)
+
+
+def test_gelu_truth_holds_in_the_tail(orc):
+    # Relative accuracy on [−30, 12] against the reference's formula in 420-digit arithmetic: the truth
+    # keeps its relative precision where the double form ½x(1 + tanh u) cancels to −0 (x ≤ −8), down to
+    # values below double's normal range (x < −21: e^(2u) < 10⁻³⁰⁸), where both are below 1e-300.
+    xs = np.concatenate([np.linspace(-30, 12, 2101), [-8.0, -9.5, -10.0, -20.0]])
+    got = np.array([orc.lib().orc_gelu_tanh(float(v)) for v in xs])
+    want = np.array([_gelu_tanh_decimal(float(v)) for v in xs])
+    # e^(−2u) carries the relative rounding of its argument times |2u| (the function's own conditioning).
+    u = math.sqrt(2 / math.pi) * (xs + 0.044715 * xs ** 3)
+    assert np.all(np.abs(got - want) <= 1e-15 * (1 + 2 * np.abs(u)) * np.abs(want) + 1e-300)
+    assert np.all(np.signbit(got[xs < 0])) and np.all(got[(xs < 0) & (xs > -21)] < 0)
+    # The double literal form gives −0 at −8; the value there is a normal number, about x·e^(2u).
+    x = -8.0
+    u = math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)
+    assert 0.5 * x * (1 + math.tanh(u)) == 0.0
+    assert math.isclose(orc.lib().orc_gelu_tanh(x), x * math.exp(2 * u), rel_tol=1e-15)
+    assert -4e-21 < orc.lib().orc_gelu_tanh(x) < -2e-21
 
 
 def test_channel_error_closed_forms(orc):
