@@ -37,6 +37,8 @@ enum sq8_status {
     SQ8_EINVAL = 1,        /* a null pointer, a negative size, a stride shorter than a row */
     SQ8_EUNSUPPORTED = 2,  /* a valid configuration this library does not run */
     SQ8_ENODEVICE = 3,     /* no gfx950 device at that ordinal */
+    SQ8_ECAPACITY = 4,     /* the problem needs more than the static scratch holds
+                              (sq8_linear_quantized_static only) */
 };
 
 /* ---- element types (Artifact.DType, Sources/Siliconed/Artifact.swift:65-113) ---- */
@@ -266,6 +268,28 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
                          const void *w, int w_layout, int64_t ldw,
                          const float *scale, int scale_layout, const float *bias, int epilogue,
                          void *c, int c_dtype, int64_t ldc, int m, int k, int n, double *gpu_seconds);
+
+/* **The W8A8 route whole, allocating nothing.** No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Arguments, arithmetic and results as sq8_linear_quantized (the same kernels, the
+ * same bits), but the activation's codes and row scales go to a static scratch array of
+ * SQ8_STATIC_SCRATCH_BYTES on each GPU, held from the library's load until the process ends, instead
+ * of the context's growable scratch; nothing is allocated or freed and the stream is never
+ * synchronized by the call. Limits: the codes (m rows of k rounded up to 128, the total rounded up to
+ * 256 bytes) and 4·m bytes of row scales must fit (else SQ8_ECAPACITY), and the weight must be
+ * packed (SQ8_PACKED / SQ8_PACKED_GLU) or [N, K] int8 with k % 128 == 0, ldw % 16 == 0 and a 16-byte
+ * aligned base, the layouts the kernel reads in place (else SQ8_EUNSUPPORTED: a repack would need a
+ * buffer). Every call on one GPU shares that GPU's array and leaves its codes there: calls that
+ * overlap on one GPU (contexts on different streams) race and must be ordered by the caller. */
+#define SQ8_STATIC_SCRATCH_BYTES (64ll << 20)
+int sq8_linear_quantized_static(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group,
+                                const void *w, int w_layout, int64_t ldw,
+                                const float *scale, int scale_layout, const float *bias, int epilogue,
+                                void *c, int c_dtype, int64_t ldc, int m, int k, int n,
+                                double *gpu_seconds);
+
+/* The static scratch's capacity in bytes (SQ8_STATIC_SCRATCH_BYTES). */
+int64_t sq8_static_scratch_bytes(void);
 
 /* **A product added into the residual stream**: x[m, n] += gate ⊙ (s ⊙ (A·W) + b), x fp32 (leading
  * dimension ldx) read and written in place, gate fp32 [n] or NULL (1), the sum in fp32 (not rounded

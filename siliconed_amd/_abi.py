@@ -12,7 +12,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libsiliconed_q8.so")
 
 # Values of include/siliconed_q8.h.
-OK, EINVAL, EUNSUPPORTED, ENODEVICE = 0, 1, 2, 3
+OK, EINVAL, EUNSUPPORTED, ENODEVICE, ECAPACITY = 0, 1, 2, 3, 4
 BF16, F32, INT8, FP8_E4M3, F16 = 1, 2, 3, 4, 5
 KN, NK, PACKED, PACKED_GLU = 0, 1, 2, 3
 SCALE_TENSOR, SCALE_COLUMNS, SCALE_BLOCKS, SCALE_ROWS = 0, 1, 2, 3
@@ -38,6 +38,9 @@ SIGNATURES = {
                              ctypes.POINTER(_D)]),
     "sq8_linear_quantized": (_I, [_P, _P, _I, _I64, _I, _P, _I, _I64, _P, _I, _P, _I, _P, _I, _I64, _I, _I, _I,
                                   ctypes.POINTER(_D)]),
+    "sq8_linear_quantized_static": (_I, [_P, _P, _I, _I64, _I, _P, _I, _I64, _P, _I, _P, _I, _P, _I, _I64, _I, _I,
+                                         _I, ctypes.POINTER(_D)]),
+    "sq8_static_scratch_bytes": (_I64, []),
     "sq8_linear_w8a8_qkv": (_I, [_P, _P, _I64, _P, _P, _I, _I64, _P, _I, _P, _P, _P, _P, _I, _I64, _I, _I, _I, _I,
                                  ctypes.POINTER(_D)]),
     "sq8_norm_modulate_rotated": (_I, [_P, _P, _I64, _P, _P, _P, ctypes.c_float, _I, _P, _I64, _P, _I64, _I, _I]),

@@ -10,9 +10,16 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 
 #include "sq8_gemm.h"
+
+// The allocation-free entry point's device memory (sq8_linear_quantized_static): one array per GPU,
+// held from the library's load until the process ends. Host code never names it in device work: the
+// name is a host-side stand-in; its device address on each GPU comes from hipGetSymbolAddress, taken
+// once per device (static_scratch_of) and used wherever a kernel or a copy needs the memory.
+static __device__ __align__(256) uint8_t scratch[SQ8_STATIC_SCRATCH_BYTES];
 
 struct sq8_ctx {
     int device;
@@ -28,6 +35,27 @@ struct sq8_ctx {
 namespace {
 
 int hip_status(hipError_t e) { return e == hipSuccess ? SQ8_OK : -(int)e; }
+
+// The static scratch's device address per device ordinal, looked up once with that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mutex;
+uint8_t *g_static_ptr[kMaxDevices];
+
+// The address of `scratch` on `device` (the current device), looked up on the first call for it.
+hipError_t static_scratch_of(int device, uint8_t **out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_static_mutex);
+    if (!g_static_ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_static_ptr[device] = static_cast<uint8_t *>(p);
+    }
+    *out = g_static_ptr[device];
+    return hipSuccess;
+}
 
 // Makes the context's device current for the scope, restoring the caller's afterwards.
 struct DeviceScope {
@@ -319,6 +347,7 @@ struct W8A8 {
     void *c[3]; int c_dtype; int64_t ldc; int split; int head_dim;
     int m, k, n;
     bool residual; const float *gate;  // c (fp32) += gate ⊙ (…), in place
+    bool no_alloc;  // the codes and row scales in the static scratch; no allocation, no repack
 };
 
 int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
@@ -354,12 +383,23 @@ int run_w8a8(sq8_ctx *ctx, const W8A8 &q, double *gpu_seconds) {
     const bool own_codes = q.a || q.k % 128 != 0 || q.ldq % 16 != 0 || !aligned(q.codes, 16);
     const size_t code_bytes = own_codes ? ((size_t)q.m * (size_t)k_pad + 255) / 256 * 256 : 0;
     const size_t bytes = code_bytes + (q.a ? (size_t)q.m * 4 : 0);
-    if (bytes > 0) {
+    uint8_t *scr = nullptr;
+    if (q.no_alloc) {
+        // The static scratch: its capacity is the limit, and the weight must be one the kernel reads
+        // as it lies (packed, or [N, K] with whole 128-code rows), since a repack would need a buffer.
+        if (bytes > (size_t)SQ8_STATIC_SCRATCH_BYTES) return SQ8_ECAPACITY;
+        if (!(is_packed(q.w_layout) ||
+              (q.w_layout == SQ8_NK && !is_glu(q.epilogue) && q.k % 128 == 0 && q.ldw % 16 == 0 && aligned(q.w, 16))))
+            return SQ8_EUNSUPPORTED;
+        const hipError_t e = static_scratch_of(ctx->device, &scr);
+        if (e != hipSuccess) return hip_status(e);
+    } else if (bytes > 0) {
         st = reserve_scratch(ctx, bytes);
         if (st != SQ8_OK) return st;
+        scr = static_cast<uint8_t *>(ctx->scratch);
     }
-    int8_t *codes = own_codes ? static_cast<int8_t *>(ctx->scratch) : const_cast<int8_t *>(q.codes);
-    const float *sx = q.a ? reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + code_bytes) : q.sx;
+    int8_t *codes = own_codes ? reinterpret_cast<int8_t *>(scr) : const_cast<int8_t *>(q.codes);
+    const float *sx = q.a ? reinterpret_cast<float *>(scr + code_bytes) : q.sx;
     const int64_t ldq = own_codes ? k_pad : q.ldq;
     if (gpu_seconds) {
         hipError_t e = hipEventRecord(ctx->begin, ctx->stream);
@@ -654,6 +694,7 @@ const char *sq8_status_string(int status) {
     case SQ8_EINVAL: return "invalid argument";
     case SQ8_EUNSUPPORTED: return "configuration not supported by this library";
     case SQ8_ENODEVICE: return "no gfx950 device at that ordinal";
+    case SQ8_ECAPACITY: return "the problem exceeds the static scratch (SQ8_STATIC_SCRATCH_BYTES)";
     default: return status < 0 ? hipGetErrorString((hipError_t)(-status)) : "unknown status";
     }
 }
@@ -675,6 +716,8 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
     memset(ctx, 0, sizeof(*ctx));
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
+    uint8_t *unused = nullptr;
+    (void)static_scratch_of(device, &unused);  // set-up; sq8_linear_quantized_static retries and reports
     e = hipEventCreate(&ctx->begin);
     if (e == hipSuccess) e = hipEventCreate(&ctx->end);
     if (e != hipSuccess) {
@@ -912,6 +955,25 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
     if (!a) return m == 0 ? SQ8_OK : SQ8_EINVAL;
     return run_w8a8(ctx, q, gpu_seconds);
 }
+
+int sq8_linear_quantized_static(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, int group, const void *w,
+                                int w_layout, int64_t ldw, const float *scale, int scale_layout, const float *bias,
+                                int epilogue, void *c, int c_dtype, int64_t ldc, int m, int k, int n,
+                                double *gpu_seconds) {
+    if (!a && m > 0) return SQ8_EINVAL;
+    W8A8 q;
+    memset(&q, 0, sizeof(q));
+    q.a = a; q.a_dtype = a_dtype; q.lda = lda; q.group = group;
+    q.w = w; q.w_layout = w_layout; q.ldw = ldw;
+    q.scale = scale; q.scale_layout = scale_layout; q.bias = bias; q.epilogue = epilogue;
+    q.c[0] = c; q.c_dtype = c_dtype; q.ldc = ldc;
+    q.m = m; q.k = k; q.n = n;
+    q.no_alloc = true;
+    if (!a) return m == 0 ? SQ8_OK : SQ8_EINVAL;
+    return run_w8a8(ctx, q, gpu_seconds);
+}
+
+int64_t sq8_static_scratch_bytes(void) { return (int64_t)SQ8_STATIC_SCRATCH_BYTES; }
 
 int64_t sq8_packed_bytes(int k, int n, int glu) {
     if (k < 0 || n < 0 || (glu && (n % 2) != 0)) return -1;

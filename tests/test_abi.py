@@ -45,6 +45,8 @@ def test_status_strings_and_version():
     assert lib.sq8_abi_version() == 1
     assert lib.sq8_status_string(0) == b"ok"
     assert b"not supported" in lib.sq8_status_string(2)
+    assert b"static scratch" in lib.sq8_status_string(4)
+    assert lib.sq8_static_scratch_bytes() == 64 << 20
 
 
 def test_null_context_is_refused_not_crashed():
@@ -60,6 +62,8 @@ def test_null_context_is_refused_not_crashed():
                               None) == _abi.EINVAL
     assert lib.sq8_linear_bf16_weight(None, None, 2, 64, None, 0, 64, None, 64, 1, 64, 64, None) == _abi.EINVAL
     assert lib.sq8_create(0, None, None) == _abi.EINVAL
+    assert lib.sq8_linear_quantized_static(None, None, 2, 64, 0, None, 1, 64, None, 1, None, 0, None, 1, 64, 1, 64,
+                                           64, None) == _abi.EINVAL
 
 
 def test_create_without_gfx950_says_no_device():
