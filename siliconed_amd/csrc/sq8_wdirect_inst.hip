@@ -1,6 +1,7 @@
 // sq8_wdirect_inst.hip — instantiates the weight-direct kernels for one weight type (SQ8_WT) and
 // layout (SQ8_WL: 1 [N, K], 2 packed), compiled once per pair so the sets build in parallel.
 #include "sq8_skinny_kernel.h"
+#include "sq8_w256_kernel.h"
 
 #if !defined(SQ8_WT) || !defined(SQ8_WL)
 #error "compile with -DSQ8_WT=<0 int8 | 1 fp8> -DSQ8_WL=<1 [N,K] | 2 packed>"
@@ -13,7 +14,12 @@ namespace sq8 {
 
 hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const GemmArgs &p, int tile, int epi, int out,
                                                                        hipStream_t stream) {
-    if (tile == WD_256) return wd::dispatch_wd<256, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    // 256 × 256 tiles where their kernel serves the product (bf16 out, plain or GELU, whole slabs); else
+    // the two-workgroup 128-row tiles.
+    if (tile == WD_256) {
+        if (wd::w256_fits(p, epi, out)) return wd::launch_w256<SQ8_WT, SQ8_WL>(p, epi, stream);
+        tile = WD_128;
+    }
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_64) return wd::dispatch_wd<64, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_32) return wd::dispatch_wd<32, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);

@@ -273,7 +273,72 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
     flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT>
+// The bf16 epilogue of one whole 64-column slab (columns [col0, col0 + 64) of the product, in one
+// output and one head): scale, bias and activation in registers; the wave's 32·FM × 64 outputs are
+// written to its LDS region (rows of 128 bytes, 16-byte chunks XOR-swizzled by row & 7) and read
+// back as 16-byte chunks, eight lanes a row, so each store instruction writes eight whole 128-byte
+// row segments. No wait between the blocks: all values are staged, then all are stored. Rows past M
+// are not stored. `region`: 32·FM·128 bytes of the wave's own.
+template <int FM, int EPI>
+__device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x16 (&acc)[2][FM], const ColParams (&cp)[2],
+                                                   bool has_bias, int m0, int col0, uint8_t *region, int lane) {
+    const int h = lane >> 5, r = lane & 31;
+    static_for<0, FM>([&](auto bmc) {
+        constexpr int bm = decltype(bmc)::value;
+        static_for<0, 2>([&](auto bc) {
+            constexpr int b = decltype(bc)::value;
+            static_for<0, 4>([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                float y[4];
+                static_for<0, 4>([&](auto ec) {
+                    constexpr int e = decltype(ec)::value;
+                    float v = __fmul_rn(acc[b][bm][4 * g + e], cp[b].s[g][e]);
+                    if (has_bias) v = __fadd_rn(v, cp[b].b[g][e]);
+                    if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
+                    y[e] = v;
+                });
+                const int row = 32 * bm + r;
+                const int chunk = 4 * b + g;  // 8 columns: 8g + [0, 8) of block b; this lane's half h
+                *reinterpret_cast<u32x2 *>(region + row * 128 + ((chunk ^ (row & 7)) << 4) + 8 * h) =
+                    u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
+            });
+        });
+    });
+    // Where the slab's rows go: output `which` of the QKV split, then row-major (ldc) or head-major
+    // ([heads, M, head_dim]: consecutive rows of one head are head_dim apart).
+    int which = 0, cc = col0;
+    if (p.split > 0) {
+        which = col0 / p.split;
+        cc = col0 - which * p.split;
+    }
+    int64_t first, pitch;
+    if (p.head_dim > 0) {
+        const int head = cc / p.head_dim;
+        first = ((int64_t)head * p.M + m0) * p.head_dim + (cc - head * p.head_dim);
+        pitch = p.head_dim;
+    } else {
+        first = (int64_t)m0 * p.ldc + cc;
+        pitch = p.ldc;
+    }
+    const int chunk = lane & 7;
+    uint8_t *const out = kern::out_base(p, which) + (first + chunk * 8) * 2;
+    static_for<0, 4 * FM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const int row = 8 * i + (lane >> 3);
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(region + row * 128 + ((chunk ^ (row & 7)) << 4));
+        if (m0 + row < p.M) *reinterpret_cast<u32x4 *>(out + (int64_t)row * pitch * 2) = v;
+    });
+}
+
+// True when a kernel's slab epilogue serves this product: bf16 output, a plain or GELU epilogue,
+// whole 64-column slabs that each lie in one output and one head, 16-byte stores.
+inline bool slab_epilogue_fits(const GemmArgs &p, int epi, int out) {
+    return (epi == EPI_NONE || epi == EPI_GELU) && out == OUT_BF16 && p.glu_half == 0 && p.N % 64 == 0 &&
+           p.split % 64 == 0 && p.head_dim % 64 == 0 && p.c_vec16;
+}
+
+// LEAN: the slab epilogue (slab_epilogue_fits holds); else each 32 × 32 block through store_block.
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
 gemm_wd_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -286,7 +351,10 @@ gemm_wd_kernel(const GemmArgs p) {
     static_assert(A_PER_WAVE + 4 < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
     // The epilogue regions lie over the A stages (both idle by then); short tiles need more than the stages.
-    constexpr int LDS_BYTES = NW * REGION > 2 * SA ? NW * REGION : 2 * SA;
+    constexpr int LDS_STAGES = NW * REGION > 2 * SA ? NW * REGION : 2 * SA;
+    // The slab epilogue stages the wave's whole BM × 64 bf16 outputs.
+    constexpr int LDS_BYTES = LEAN && NW * BM * 128 > LDS_STAGES ? NW * BM * 128 : LDS_STAGES;
+    static_assert(!LEAN || (OUT == OUT_BF16 && (EPI == EPI_NONE || EPI == EPI_GELU)), "slab epilogue: bf16, plain or GELU");
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
@@ -515,6 +583,11 @@ gemm_wd_kernel(const GemmArgs p) {
     // 32·b + 8·(r >> 2) + 4·(l >> 5) + (r & 3). The A stages are free: every wave passed the last
     // barrier after its last fragment read and after its last load into them landed.
     const int n_out = GLU ? p.glu_half : p.N;
+    if constexpr (LEAN) {
+        if (slab * 64 < p.N)
+            slab_epilogue_bf16<FM, EPI>(p, acc, cp, has_bias, m0, slab * 64, lds + wave * (BM * 128), lane);
+        return;
+    }
     uint8_t *region = lds + wave * REGION;
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
@@ -528,7 +601,7 @@ gemm_wd_kernel(const GemmArgs p) {
     });
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT>
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false>
 hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
@@ -537,12 +610,15 @@ hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = (slabs + NW - 1) / NW;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
 template <int BM, int NW, int OCC, int WT, int WL>
 hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) {
+    if (slab_epilogue_fits(p, epi, out))
+        return epi == EPI_GELU ? launch_wd<BM, NW, OCC, WT, WL, EPI_GELU, OUT_BF16, true>(p, stream)
+                               : launch_wd<BM, NW, OCC, WT, WL, EPI_NONE, OUT_BF16, true>(p, stream);
 #define SQ8_CASE(E, O)                                                                            \
     if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)

@@ -1,0 +1,100 @@
+"""The 256 × 256 kernel (one workgroup per CU) and the slab epilogue, on an MI355X.
+
+Every output of the weight-direct kernels is one MFMA sequence over K whatever the tile, and the slab
+epilogue applies the same scale, bias and activation as the 32 × 32-block one: so the 256-row tiles
+give the same bits as the 128-row tiles, and both are judged against the oracle's fp64 truth on
+sampled rows at the reference's bars (DiagnosticProbes.swift:75-82, DiagnosticJudgement.swift:39-71).
+Shapes cover a ragged last row tile, a last column tile with fewer slabs than waves, per-tensor scales,
+no bias, fp8 codes, both weight layouts, and the QKV split (row-major and head-major).
+"""
+import numpy as np
+import pytest
+import torch
+
+from refgen import bitwise_equal
+from test_gpu_parity import DEV, bf16_dev, dev, judge, problem, weight_tensor
+
+pytestmark = pytest.mark.gpu
+
+
+def product(gemm, monkeypatch, tile, x, w, s, b, layout, epi, out_dtype=torch.bfloat16):
+    monkeypatch.setenv("SQ8_TILE", tile)
+    try:
+        y = gemm.product(bf16_dev(x), w, dev(s), layout=layout, bias=None if b is None else dev(b),
+                         epilogue="gelu_tanh" if epi == "gelu" else None, out_dtype=out_dtype)
+        torch.cuda.synchronize()
+    finally:
+        monkeypatch.delenv("SQ8_TILE")
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("m,k,n,fp8,layout,epi,bias,tensor_scale", [
+    (1000, 512, 1344, False, "packed", "gelu", True, False),   # ragged rows; last column tile: 1 slab of 4
+    (512, 1024, 1024, False, "nk", "none", False, False),       # [N, K] codes read in place, no bias
+    (777, 768, 640, True, "packed", "none", True, False),       # fp8, ragged rows, 2 + 2 + 2... slabs
+    (256, 2048, 768, True, "nk", "gelu", True, True),           # fp8 in place, one scale for the tensor
+    (1, 512, 512, False, "packed", "gelu", True, False),        # one row
+])
+def test_w256_same_bits_as_128(gemm, orc, monkeypatch, m, k, n, fp8, layout, epi, bias, tensor_scale):
+    x, q, s, b = problem(orc, m, k, n, fp8, 400 + m + n, bias=bias)
+    if tensor_scale:
+        s = np.array([float(np.median(s))], dtype=np.float32)
+    w = weight_tensor(q, fp8, "nk")
+    if layout == "packed":
+        w = gemm.pack(w, layout="nk")
+    y256 = product(gemm, monkeypatch, "256", x, w, s, b, "nk", epi)
+    y128 = product(gemm, monkeypatch, "128", x, w, s, b, "nk", epi)
+    assert bitwise_equal(y256, y128) == 0
+    sj = np.full(n, s[0], dtype=np.float32) if tensor_scale else s
+    judge(orc, y256, x, q, fp8, sj, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+def test_w256_fp32_output_takes_128(gemm, orc, monkeypatch):
+    """An fp32 output is not the 256 kernel's: the product falls back to 128-row tiles, same bits."""
+    m, k, n = 600, 512, 768
+    x, q, s, b = problem(orc, m, k, n, False, 91)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    y256 = product(gemm, monkeypatch, "256", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
+    y128 = product(gemm, monkeypatch, "128", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
+    assert bitwise_equal(y256, y128) == 0
+    judge(orc, y256, x, q, False, s, b, "gelu", torch.float32, rows=orc.sample_rows(m, 64))
+
+
+@pytest.mark.parametrize("head_dim", [0, 128, 64])
+def test_w256_qkv(gemm, orc, monkeypatch, head_dim):
+    """The fused QKV product on 256-row tiles: each 64-column slab lies in one output and one head, its
+    rows stored row-major or head-major; the same bits as the 128-row tiles, each third judged."""
+    m, k, d = 700, 512, 384
+    x, q, s, b = problem(orc, m, k, 3 * d, False, 77 + head_dim)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    outs = {}
+    for tile in ("256", "128"):
+        monkeypatch.setenv("SQ8_TILE", tile)
+        try:
+            qq, kk, vv = gemm.product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
+            torch.cuda.synchronize()
+        finally:
+            monkeypatch.delenv("SQ8_TILE")
+        parts = []
+        for t in (qq, kk, vv):
+            t = t.float()
+            if head_dim:
+                t = t.permute(1, 0, 2).reshape(m, d)  # [heads, m, hd] → [m, d]
+            parts.append(t.cpu().numpy())
+        outs[tile] = np.concatenate(parts, axis=1)
+    assert bitwise_equal(outs["256"], outs["128"]) == 0
+    judge(orc, outs["256"], x, q, False, s, b, "none", torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+def test_slab_epilogue_same_bits_as_block_epilogue(gemm, orc):
+    """The slab epilogue (16-byte aligned bf16 rows) against the 32 × 32-block epilogue (the same product
+    into rows whose stride is not a multiple of 8 bf16, which the slab epilogue does not take)."""
+    m, k, n = 900, 1024, 1536
+    x, q, s, b = problem(orc, m, k, n, False, 55)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    lean = gemm.product(bf16_dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh")
+    wide = torch.empty((m, n + 4), dtype=torch.bfloat16, device=DEV)
+    block = gemm.product(bf16_dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh", out=wide[:, :n])
+    torch.cuda.synchronize()
+    assert bitwise_equal(lean.float().cpu().numpy(), block.float().cpu().numpy()) == 0
+    judge(orc, lean.float().cpu().numpy(), x, q, False, s, b, "gelu", torch.bfloat16, rows=orc.sample_rows(m, 64))
