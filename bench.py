@@ -232,7 +232,7 @@ def launch_stats(times_ms) -> dict:
 def c4_measure(route: str, steps: int, warmup: int, settle_ms: float) -> dict:
     """One synthetic single-stream DiT block forward (siliconed_amd.dit_block) on `route` ("bf16", or
     "w8a8" with convrot 256): hidden 3072, 24 heads of 128, 4096 image + 512 text tokens. Each timed
-    forward is bracketed by its own HIP events; returns the mean, min and median ms."""
+    forward is bracketed by its own HIP events; returns the median forward as `ms`, the mean beside it."""
     import torch
     from siliconed_amd.dit_block import DiTBlock
     S, d, heads = 4096 + 512, 3072, 24
@@ -257,10 +257,14 @@ def c4_measure(route: str, steps: int, warmup: int, settle_ms: float) -> dict:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    ms = ev[0].elapsed_time(ev[steps]) / steps
+    mean = ev[0].elapsed_time(ev[steps]) / steps
+    # The median forward: a host-side stall between two launches (the GPU then idles until the next one
+    # is queued) lands in one forward's events and would move the mean, not the median.
+    ms = float(np.median(per))
     flops = blk.flops(S)
-    out = {"ms": round(ms, 4), "per_forward_ms": launch_stats(per), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-           "flops": flops, "steps": steps, "warmup": warmup, "wall_ms_per_step": round(1e3 * wall / steps, 4), **st}
+    out = {"ms": round(ms, 4), "mean_ms": round(mean, 4), "per_forward_ms": launch_stats(per),
+           "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "flops": flops, "steps": steps, "warmup": warmup,
+           "wall_ms_per_step": round(1e3 * wall / steps, 4), **st}
     del blk, streams, work, x
     torch.cuda.empty_cache()
     return out
@@ -270,7 +274,7 @@ def dit_block(args) -> int:
     """C4: one synthetic single-stream DiT block forward (siliconed_amd.dit_block): hidden 3072, 24
     heads of 128, 4096 image + 512 text tokens, int8 per-channel modulation / QKV / out / MLP-4×
     weights, bf16 attention, fp32 residual. value: the block's forward time in ms (HIP events over the
-    timed forwards); `tflops` beside it (linear + attention FLOPs over that time)."""
+    timed forwards, the median forward); `tflops` beside it (linear + attention FLOPs over that time)."""
     S, d, heads = 4096 + 512, 3072, 24
     w8a8 = args.workload == "c4_block_w8a8"
     steps = max(args.steps // 2, 5)
@@ -281,7 +285,7 @@ def dit_block(args) -> int:
         "metric": ("DiT block forward ms (hidden 3072, 24x128 heads, 4608 tokens, int8 weights"
                    + (", W8A8 route, convrot 256" if w8a8 else "") + ") on 1 MI355X"),
         "value": round(ms, 4), "unit": "ms", "tflops": round(tflops, 2), "n_gpus": 1, "steps": steps,
-        "warmup": warm, "settle_ms": r["settle_ms"], "per_forward_ms": r["per_forward_ms"],
+        "warmup": warm, "settle_ms": r["settle_ms"], "mean_ms": r["mean_ms"], "per_forward_ms": r["per_forward_ms"],
         "ms_per_step": r["wall_ms_per_step"], "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if w8a8 else "bf16",
         "data": f"synthetic, seeded: x, temb SplitMix64 + Box-Muller; weights torch generator seed {SEEDS['w']}",
@@ -523,7 +527,7 @@ def main() -> int:
         for route in ("bf16", "w8a8"):
             r = c4_measure(route, steps=10, warmup=2, settle_ms=min(args.settle_ms, 300.0))
             result[f"c4_block_{route}_ms"] = r["ms"]
-            result[f"c4_block_{route}"] = {k: r[k] for k in ("per_forward_ms", "tflops", "steps", "settle_ms")}
+            result[f"c4_block_{route}"] = {k: r[k] for k in ("mean_ms", "per_forward_ms", "tflops", "steps", "settle_ms")}
     if not args.no_cpu:
         xb = x.view(torch.int16).numpy()
         result["cpu_baseline"] = cpu_baseline(args.workload, xb, q.view(torch.uint8).numpy() if fp8 else q, s, b,

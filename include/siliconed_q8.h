@@ -82,6 +82,11 @@ typedef struct sq8_ctx sq8_ctx;
 
 /* Creates a context on HIP device `device`, launching on `stream` (a hipStream_t; NULL = the
  * device's null stream). Refuses (SQ8_ENODEVICE) a device that is not gfx950.
+ * Two measurement knobs are read from the environment here, once per context: SQ8_TILE ("256",
+ * "128", "64", "32", "s64", "s32": the weight-direct kernels' tile) and SQ8_Q8_TILE ("256", "512",
+ * "128x256", "128x128": the block-scale kernel's tile). A context created with one set runs every
+ * product of that family on that tile (a tile that cannot serve a product falls back to the nearest
+ * one that can); unset, the library chooses per product.
  * Replaces: TensorGEMM.init?(device:queue:roundingActivations:quantizingActivations:)
  * (Sources/Siliconed/TensorGEMM.swift:206-232). */
 int sq8_create(int device, void *stream, sq8_ctx **out);
@@ -109,7 +114,11 @@ int sq8_supports(const sq8_ctx *ctx, int a_dtype, int w_dtype, int w_layout, int
  * `ldw`/`ldc` say so (the `columns` argument of `submit`, TensorGEMM.swift:296).
  * `gpu_seconds`: NULL → the launch is queued and the call returns at once (`settled`,
  * TensorGEMM.swift:261-263); non-NULL → the call waits and writes the kernel's GPU seconds
- * (TensorGEMM.swift:268-272, `Attention.verdict`).
+ * (TensorGEMM.swift:268-272, `Attention.verdict`). One exception to "at once": the context's two
+ * growable buffers — the bf16 copy (or, on the fp32 route, the three parts) of an fp32 A, and the
+ * repack of [K, N] codes read in place — are sized by the largest product so far; a call that needs
+ * more first synchronizes the context's stream (queued work may still read the old buffer), frees
+ * and allocates. A caller that must never block runs one product of its largest shape first.
  * Replaces: TensorGEMM.linear(a:int8:weightOffset:scales:scalesOffset:perColumn:block:rotation:
  * rounding:quantizing:prequantized:c:m:k:n:settled:) -> Double (TensorGEMM.swift:264-290) and
  * its encoders submit (:296-360) / submitRounded (TensorGEMMBF16.swift:208-264), with the bias
@@ -365,7 +374,8 @@ int sq8_gated_residual(sq8_ctx *ctx, float *x, int64_t ldx, const void *y, int y
 
 /* **The product on block scales**: C[m, n_out] = act(A · W + b), W[k, c] = q[k, c] · s[k / block, c],
  * int8 codes q, `block` a multiple of 32 dividing k (Q8_0: 32), k a multiple of 64. Codes in
- * `w_layout` SQ8_KN ([k, n], scales [k/block, n] row-major — the map's `[K/b, N]`) or SQ8_NK
+ * `w_layout` SQ8_KN ([k, n], scales [k/block, n] row-major with the codes' row stride `ldw` — the
+ * map's `[K/b, N]`; n < ldw computes the first n columns, `submit(…columns:)`) or SQ8_NK
  * ([n, k], scales [n, k/block] — GGUF's rows of blocks), scales of `scale_dtype` SQ8_F32, SQ8_BF16
  * or SQ8_F16 (widened exactly); or SQ8_PACKED(_GLU): `w` written by sq8_pack_blocks, which holds the
  * scales (`scale`, `scale_dtype`, `ldw` ignored). Each block's fp32 partial sum of exact bf16 × code

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <mutex>
 #include <new>
 
@@ -30,6 +31,8 @@ struct sq8_ctx {
     void *wpack;            // [K, N] codes repacked for the weight-direct kernels, per product
     size_t wpack_bytes;
     rocblas_handle blas;    // the bf16-weight product's library GEMM (created on its first call)
+    int wd_tile;            // measurement knobs, read once at sq8_create (SQ8_TILE, SQ8_Q8_TILE): a forced
+    int q8_tile;            // weight-direct / block-scale tile, or -1 (the product's own choice)
 };
 
 namespace {
@@ -72,6 +75,19 @@ struct DeviceScope {
 };
 
 bool aligned(const void *p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// A measurement knob's value (an environment variable read when a context is created): the tile named,
+// or -1 when unset or unknown (the product's own choice).
+struct KnobValue {
+    const char *name;
+    int tile;
+};
+int knob(const char *value, std::initializer_list<KnobValue> table) {
+    if (!value) return -1;
+    for (const KnobValue &v : table)
+        if (strcmp(value, v.name) == 0) return v.tile;
+    return -1;
+}
 
 bool is_glu(int epilogue) { return epilogue == SQ8_EPI_SILU_GLU || epilogue == SQ8_EPI_SITU_GLU; }
 
@@ -221,15 +237,8 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         if (st != SQ8_OK) return st;
         const float *x = static_cast<const float *>(q.a);
         uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
-        if (q.lda == q.k) {
-            hipError_t e = sq8::launch_round_bf16(x, y, (int64_t)q.m * q.k, ctx->stream);
-            if (e != hipSuccess) return hip_status(e);
-        } else {
-            for (int r = 0; r < q.m; ++r) {
-                hipError_t e = sq8::launch_round_bf16(x + (int64_t)r * q.lda, y + (int64_t)r * q.k, q.k, ctx->stream);
-                if (e != hipSuccess) return hip_status(e);
-            }
-        }
+        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
         p.a = y;
         p.lda = q.k;
     }
@@ -306,14 +315,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
-        int tile = sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
-        const char *force = getenv("SQ8_TILE");  // measurement knob: "256", "128", "64", "32", "s64", "s32"
-        if (force && strcmp(force, "256") == 0) tile = sq8::WD_256;
-        if (force && strcmp(force, "128") == 0) tile = sq8::WD_128;
-        if (force && strcmp(force, "64") == 0) tile = sq8::WD_64;
-        if (force && strcmp(force, "32") == 0) tile = sq8::WD_32;
-        if (force && strcmp(force, "s64") == 0) tile = sq8::WD_SKINNY64;
-        if (force && strcmp(force, "s32") == 0) tile = sq8::WD_SKINNY32;
+        const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
         e = sq8::launch_wdirect(p, tile, wt, wl, epi, out, ctx->stream);
     } else if (q.residual || q.exact) {
         return SQ8_EUNSUPPORTED;  // the residual epilogue and the fp32 route run on the weight-direct kernels only
@@ -546,11 +548,8 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
         if (st != SQ8_OK) return st;
         const float *x = static_cast<const float *>(q.a);
         uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
-        for (int r = 0; r < (q.lda == q.k ? 1 : q.m); ++r) {
-            const int64_t count = q.lda == q.k ? (int64_t)q.m * q.k : q.k;
-            hipError_t e = sq8::launch_round_bf16(x + (int64_t)r * q.lda, y + (int64_t)r * q.k, count, ctx->stream);
-            if (e != hipSuccess) return hip_status(e);
-        }
+        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, ctx->stream);
+        if (e != hipSuccess) return hip_status(e);
         p.a = y;
         p.lda = q.k;
     }
@@ -584,12 +583,7 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     p.c_vec16 = aligned(q.c, 16) && (q.ldc % (int64_t)(16 / esz)) == 0;
     // 128-row tiles of one 32-column block per wave (the codes widened once for twice the rows);
     // the GLU epilogues pair both blocks of a slab in one wave: 64-row tiles.
-    int tile = is_glu(q.epilogue) ? sq8::BL_64x256 : sq8::BL_128x256;
-    const char *force = getenv("SQ8_Q8_TILE");  // measurement knob: "256", "512", "128x256", "128x128"
-    if (force && strcmp(force, "256") == 0) tile = sq8::BL_64x256;
-    if (force && strcmp(force, "512") == 0) tile = sq8::BL_64x512;
-    if (force && strcmp(force, "128x256") == 0) tile = sq8::BL_128x256;
-    if (force && strcmp(force, "128x128") == 0) tile = sq8::BL_128x128;
+    const int tile = ctx->q8_tile >= 0 ? ctx->q8_tile : is_glu(q.epilogue) ? sq8::BL_64x256 : sq8::BL_128x256;
     hipError_t e = sq8::launch_blocks_product(p, tile, q.epilogue, q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16,
                                   ctx->stream);
     if (e != hipSuccess) return hip_status(e);
@@ -716,6 +710,10 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
     memset(ctx, 0, sizeof(*ctx));
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
+    ctx->wd_tile = knob(getenv("SQ8_TILE"), {{"256", sq8::WD_256}, {"128", sq8::WD_128}, {"64", sq8::WD_64},
+                                             {"32", sq8::WD_32}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32}});
+    ctx->q8_tile = knob(getenv("SQ8_Q8_TILE"), {{"256", sq8::BL_64x256}, {"512", sq8::BL_64x512},
+                                                {"128x256", sq8::BL_128x256}, {"128x128", sq8::BL_128x128}});
     uint8_t *unused = nullptr;
     (void)static_scratch_of(device, &unused);  // set-up; sq8_linear_quantized_static retries and reports
     e = hipEventCreate(&ctx->begin);

@@ -52,6 +52,17 @@ __global__ void __launch_bounds__(256) round_bf16_kernel(const float *__restrict
         y[i] = (uint16_t)round_bf16(x[i]);
 }
 
+// The same rounding of `rows` rows of k values read `ldx` apart, written k apart (a strided fp32 operand
+// into the packed bf16 copy the products read).
+__global__ void __launch_bounds__(256) round_bf16_rows_kernel(const float *__restrict__ x, int64_t ldx,
+                                                              uint16_t *__restrict__ y, int64_t rows, int k) {
+    const int64_t count = rows * k;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / k;
+        y[i] = (uint16_t)round_bf16(x[r * ldx + (i - r * k)]);
+    }
+}
+
 // fp32 → three bf16 parts along K: y[r, k] = hi, y[r, K + k] = mid, y[r, 2K + k] = lo, each part the top
 // 16 bits of what the one before leaves (hi = x truncated to bf16, mid = (x − hi) truncated, lo = x − hi − mid):
 // 24 significant bits in three parts of 8, every difference exact, no part rounded, so hi + mid + lo = x and
@@ -219,6 +230,13 @@ hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows,
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream) {
     if (count == 0) return hipSuccess;
     hipLaunchKernelGGL(round_bf16_kernel, dim3(grid_for(count)), dim3(256), 0, stream, x, y, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream) {
+    if (rows == 0 || k == 0) return hipSuccess;
+    if (ldx == k) return launch_round_bf16(x, y, rows * k, stream);
+    hipLaunchKernelGGL(round_bf16_rows_kernel, dim3(grid_for(rows * k)), dim3(256), 0, stream, x, ldx, y, rows, k);
     return hipGetLastError();
 }
 

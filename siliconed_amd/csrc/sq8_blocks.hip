@@ -29,8 +29,8 @@ __device__ __forceinline__ int weight_column(int slab, int vc, int n, int glu) {
 
 // One thread per 16-byte chunk: the code chunks first (chunks of the packed layout, block-aligned K
 // order), then the scale chunks ((slab·kt + t)·32 + nl). Codes [K, N] (wl W_KN) or [N, K] (W_NK);
-// scales [K/B, N] for W_KN, [N, K/B] for W_NK (each layout's own orientation: the map's blocks,
-// GGUF's rows of blocks).
+// scales [K/B, ·] with the codes' row stride ldw for W_KN (n ≤ ldw: the first n columns of a wider
+// weight), [N, K/B] for W_NK (each layout's own orientation: the map's blocks, GGUF's rows of blocks).
 __global__ void __launch_bounds__(256) pack_blocks_kernel(const uint8_t *__restrict__ w, int wl, int64_t ldw,
                                                           const void *__restrict__ scale, int scale_kind, int block,
                                                           int k, int n, int glu, int kt, int64_t code_chunks,
@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(256) pack_blocks_kernel(const uint8_t *__restr
                 float s = 0.0f;
                 if (col >= 0 && k0 < k) {
                     const int blk = k0 / block;
-                    s = scale_value(scale, scale_kind, wl == W_KN ? (int64_t)blk * n + col : (int64_t)col * kb_count + blk);
+                    s = scale_value(scale, scale_kind, wl == W_KN ? (int64_t)blk * ldw + col : (int64_t)col * kb_count + blk);
                 }
                 v[q] = s;
             }

@@ -49,8 +49,10 @@ hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, i
 // kernel with 64- or 32-row tiles of one 64-column slab and the K steps split over four waves
 // (WD_SKINNY64, WD_SKINNY32).
 enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 4, WD_32 = 5 };
-// The tile for an M × N product (GLU: N = 2h): the tallest of 128, 64 and 32 rows whose tiles number at
-// least 144 (enough to occupy the 256 CUs), else the skinny kernel.
+// The tile for an M × N product (GLU: N = 2h): 256 × 256 while those tiles make at least two rounds on
+// the 256 CUs (non-GLU; launch_wdirect takes 128-row tiles where the 256 kernel cannot serve the
+// product), else the tallest of 128, 64 and 32 rows whose tiles number at least 144 (enough to occupy
+// the 256 CUs), else the skinny kernel.
 int choose_wd_tile(int M, int N, bool glu);
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
 
@@ -81,6 +83,8 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
                              int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out,
                              hipStream_t stream);
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
+// rows × k values read ldx apart → rows × k bf16 written k apart (one launch, any stride).
+hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream);
 // fp32 [rows, k] (leading dimension ldx) → bf16 [rows, 3k]: the three parts hi | mid | lo of each value
 // (each the top 16 bits of what the one before leaves: hi + mid + lo = x, no part rounded), the fp32 route's
 // operand.

@@ -50,7 +50,9 @@ class DiTBlock:
     """The block's weights (int8 packed, fp32 scales, fp32 norm weights) on one device."""
 
     def __init__(self, d: int = 3072, heads: int = 24, mlp: int = 4, seed: int = 0, device: int = 0,
-                 ctx: TensorGEMM | None = None, route: str = "bf16", group: int = 0):
+                 ctx: TensorGEMM | None = None, route: str = "bf16", group: int = 0, keep_codes: bool = False):
+        """`keep_codes`: also keep each weight's int8 codes [N, K] (key "q") beside the packed copy the
+        forward reads — for a checker that widens them itself; off, only the packed codes stay resident."""
         if d % heads or (d // heads) % 8:
             raise ValueError("d must split into heads of a multiple of 8")
         if route not in ("bf16", "w8a8"):
@@ -64,7 +66,10 @@ class DiTBlock:
         def linear(n_out: int, k: int):
             q, s = quantize_int8(torch.randn((n_out, k), device=dev, generator=g) * 0.02)
             b = torch.randn(n_out, device=dev, generator=g) * 0.02
-            return {"q": q, "s": s, "b": b, "packed": self.ctx.pack(q, layout="nk")}
+            lin = {"n": n_out, "s": s, "b": b, "packed": self.ctx.pack(q, layout="nk")}
+            if keep_codes:
+                lin["q"] = q
+            return lin
 
         self.mod = linear(6 * d, d)
         self.qkv = linear(3 * d, d)
@@ -133,5 +138,5 @@ class DiTBlock:
     def flops(self, S: int) -> float:
         """Linear FLOPs (modulation included) + attention's two products."""
         d = self.d
-        lin = 2.0 * (6 * d * d + S * (3 * d * d + d * d + 2 * self.up["q"].shape[0] * d))
+        lin = 2.0 * (6 * d * d + S * (3 * d * d + d * d + 2 * self.up["n"] * d))
         return lin + 4.0 * S * S * d

@@ -175,15 +175,16 @@ class TensorGEMM:
         `scales_offset`; `per_column` ignored), the product of sq8_linear_blocks.
 
         `columns` ≤ n: only C's first `columns` columns are computed and written (the reference's
-        `submit(…columns:)`, TensorGEMM.swift:292-296); C keeps its row stride n. Not with block
-        scales, a quantization or a GLU epilogue.
+        `submit(…columns:)`, TensorGEMM.swift:292-296); C keeps its row stride n; the weight's codes
+        and block scales keep theirs. Not with a quantization or a GLU epilogue.
         """
+        cols = n
         if columns is not None and columns != n:
             if not 0 <= columns <= n:
                 raise ValueError(f"columns = {columns} outside [0, {n}]")
-            if block is not None or quantizing is not None or prequantized is not None or \
-                    epilogue in ("silu_glu", "situ_glu"):
-                raise abi.Unsupported(abi.EUNSUPPORTED, "columns with block scales, a quantization or a GLU epilogue")
+            if quantizing is not None or prequantized is not None or epilogue in ("silu_glu", "situ_glu"):
+                raise abi.Unsupported(abi.EUNSUPPORTED, "columns with a quantization or a GLU epilogue")
+            cols = columns
         if block is not None:
             if rotation is not None or quantizing is not None or prequantized is not None or fp8:
                 raise abi.Unsupported(abi.EUNSUPPORTED, "block scales take int8 codes, no rotation, bf16 operands")
@@ -196,20 +197,21 @@ class TensorGEMM:
                     scales.numel() * 4 < scales_offset + 4 * (k // max(int(block), 1)) * n:
                 raise ValueError("scales must be fp32, [k / block, n] after the offset (a multiple of 4 bytes)")
             secs = ctypes.c_double(0.0)
+            # The first `cols` columns: the codes' and scales' strides (n, k) and C's (n_out) kept.
             if a.dtype == torch.float32 and not rounding:
                 # The fp32 route on block scales (the reference's `blocks` pipeline on fp32 A).
                 st = abi.load().sq8_linear_f32(self._h, _dev(a, "a"), k, 0, _dev(int8, "int8") + weight_offset,
                                                abi.INT8, lay, n if lay == abi.KN else k,
                                                _dev(scales, "scales") + scales_offset, abi.F32, abi.SCALE_BLOCKS,
                                                int(block), None if bias is None else _dev(bias, "bias"), epi,
-                                               _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                               _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, cols,
                                                None if settled else ctypes.byref(secs))
                 abi.check(st, "sq8_linear_f32")
                 return 0.0 if settled else secs.value
             st = abi.load().sq8_linear_blocks(self._h, _dev(a, "a"), _adtype(a), k, _dev(int8, "int8") + weight_offset,
                                               lay, n if lay == abi.KN else k, _dev(scales, "scales") + scales_offset,
                                               abi.F32, int(block), None if bias is None else _dev(bias, "bias"), epi,
-                                              _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, n,
+                                              _dev(c, "c"), _cdtype(c.dtype), n_out, m, k, cols,
                                               None if settled else ctypes.byref(secs))
             abi.check(st, "sq8_linear_blocks")
             return 0.0 if settled else secs.value
@@ -260,14 +262,15 @@ class TensorGEMM:
 
     def submit(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
                c: torch.Tensor, m: int, k: int, n: int, columns: int, weight_offset: int = 0, scales_offset: int = 0,
-               rotation=None, rounding: bool = True, layout: str = "kn", bias: Optional[torch.Tensor] = None,
-               epilogue=None, fp8: Optional[bool] = None) -> None:
+               block: Optional[int] = None, rotation=None, rounding: bool = True, layout: str = "kn",
+               bias: Optional[torch.Tensor] = None, epilogue=None, fp8: Optional[bool] = None) -> None:
         """`submit(a:int8:…:c:m:k:n:columns:)` (TensorGEMM.swift:292-360): the product on the first
         `columns` of C only, queued and not waited for — the caller computes the other columns
-        meanwhile and synchronizes before reading C."""
+        meanwhile and synchronizes before reading C. `block`: block scales, as `linear`."""
         self.linear(a, int8=int8, scales=scales, per_column=per_column, c=c, m=m, k=k, n=n,
-                    weight_offset=weight_offset, scales_offset=scales_offset, rotation=rotation, rounding=rounding,
-                    settled=True, layout=layout, bias=bias, epilogue=epilogue, fp8=fp8, columns=columns)
+                    weight_offset=weight_offset, scales_offset=scales_offset, block=block, rotation=rotation,
+                    rounding=rounding, settled=True, layout=layout, bias=bias, epilogue=epilogue, fp8=fp8,
+                    columns=columns)
 
     def linear_bf16_weight(self, a: torch.Tensor, *, w: torch.Tensor, c: torch.Tensor, m: int, k: int, n: int,
                            weight_is_transposed: bool) -> float:
@@ -287,9 +290,10 @@ class TensorGEMM:
         return secs.value
 
     def product_bf16_weight(self, x: torch.Tensor, w: torch.Tensor, *, layout: str = "nk",
-                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                            out: Optional[torch.Tensor] = None, timed: bool = False):
         """y fp32 [m, n] = x · Wᵀ for W bf16 [n, k] (`"nk"`, nn.Linear) or x · W for W [k, n] (`"kn"`);
-        x fp32 (used whole) or bf16. No scale, no bias: the bf16-weight product."""
+        x fp32 (used whole) or bf16. No scale, no bias: the bf16-weight product. Returns y (and the GPU
+        seconds on the context's stream when `timed`)."""
         m, k = x.shape
         lay = _LAYOUTS[layout]
         if w.dtype != torch.bfloat16 or w.dim() != 2 or (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
@@ -297,11 +301,12 @@ class TensorGEMM:
         n = w.shape[0] if lay == abi.NK else w.shape[1]
         if out is None:
             out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+        secs = ctypes.c_double(0.0)
         st = abi.load().sq8_linear_bf16_weight(self._h, _dev(x, "x"), _adtype(x), _row_major(x, "x"), _dev(w, "w"), lay,
                                                _row_major(w, "w"), _dev(out, "out"), _row_major(out, "out"), m, k, n,
-                                               None)
+                                               ctypes.byref(secs) if timed else None)
         abi.check(st, "sq8_linear_bf16_weight")
-        return out
+        return (out, secs.value) if timed else out
 
     def _w8a8_linear(self, a, int8, scales, per_column, c, m, k, n, weight_offset, scales_offset, group, prequantized,
                      settled, layout, bias, epilogue) -> float:

@@ -123,18 +123,17 @@ class WeightProducts:
         x = a.reshape(-1)[: m * k].view(m, k)
         out = c.reshape(-1)[: m * n_out].view(m, n_out)
         g = self.gemm
+        # The products run on the caller's current stream, ordered with its other work (the context
+        # waits for its previous stream's work when the stream changes).
+        g.set_stream(torch.cuda.current_stream(self.device))
         if r.weight == "bfloat16":
             if epilogue is not None or bias is not None:
                 raise abi.Unsupported(abi.EUNSUPPORTED, f"{name}: the bf16-weight product takes no bias or epilogue")
             w = self.staged(name)
             if r.activation == "rounded" and x.dtype == torch.float32:
                 x = g.round_bf16(x)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            g.product_bf16_weight(x, w, layout="kn", out=out)
-            e1.record()
-            e1.synchronize()
-            return e0.elapsed_time(e1) * 1e-3
+            _, secs = g.product_bf16_weight(x, w, layout="kn", out=out, timed=True)
+            return secs
         w = self.staged(name, glu=glu)
         assert isinstance(w, StagedWeight)
         if r.activation == "quantized":

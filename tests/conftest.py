@@ -28,3 +28,26 @@ def gemm():
     ctx = sq.TensorGEMM.make(0)
     assert ctx is not None, "cuda:0 is not a gfx950"
     return ctx
+
+
+@pytest.fixture(scope="session")
+def tile_gemm(gemm):
+    """knob → a context on cuda:0 created with SQ8_TILE = knob (the library reads its tile knobs once, when
+    a context is created): the product on that forced weight-direct tile. Contexts are kept per knob."""
+    import siliconed_amd as sq
+    made = {}
+
+    def get(knob: str):
+        if knob not in made:
+            old = os.environ.get("SQ8_TILE")
+            os.environ["SQ8_TILE"] = knob
+            try:
+                made[knob] = sq.TensorGEMM.make(0)
+            finally:
+                if old is None:
+                    os.environ.pop("SQ8_TILE", None)
+                else:
+                    os.environ["SQ8_TILE"] = old
+        return made[knob]
+
+    return get

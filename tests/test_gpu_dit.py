@@ -21,7 +21,7 @@ def _update_error(y, x, ref):
 @pytest.mark.parametrize("S,d,heads", [(256, 384, 3), (300, 256, 2)])
 def test_block_matches_fp32_reference(S, d, heads):
     from siliconed_amd.dit_block import DiTBlock
-    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=S)
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=S, keep_codes=True)
     g = torch.Generator(device="cuda:0").manual_seed(1)
     x = torch.randn((S, d), device="cuda:0", generator=g)
     temb = torch.randn(d, device="cuda:0", generator=g)
@@ -39,7 +39,7 @@ def test_w8a8_block_matches_fp32_reference(S, d, heads, group):
     # whose operands are quantized the same way (per row after the rotation) — the bar of the bf16
     # route: the fused attention's bf16 probabilities dominate.
     from siliconed_amd.dit_block import DiTBlock
-    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=S + group, route="w8a8", group=group)
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=S + group, route="w8a8", group=group, keep_codes=True)
     g = torch.Generator(device="cuda:0").manual_seed(2)
     x = torch.randn((S, d), device="cuda:0", generator=g)
     temb = torch.randn(d, device="cuda:0", generator=g)
@@ -58,7 +58,7 @@ def test_c4_block_at_full_size(route, group):
     from siliconed_amd.dit_block import DiTBlock
     S, d, heads = 4608, 3072, 24
     print(f"c4 full size: route {route} group {group} S {S} d {d}", flush=True)
-    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=7, route=route, group=group)
+    blk = DiTBlock(d=d, heads=heads, mlp=4, seed=7, route=route, group=group, keep_codes=True)
     g = torch.Generator(device="cuda:0").manual_seed(4)
     x = torch.randn((S, d), device="cuda:0", generator=g)
     temb = torch.randn(d, device="cuda:0", generator=g)
@@ -77,7 +77,7 @@ def test_c4_block_at_full_size(route, group):
 
 def test_block_flops():
     from siliconed_amd.dit_block import DiTBlock
-    blk = DiTBlock(d=256, heads=2, mlp=4, seed=0)
+    blk = DiTBlock(d=256, heads=2, mlp=4, seed=0, keep_codes=True)
     S, d = 100, 256
     assert blk.flops(S) == 2.0 * (6 * d * d + S * 12 * d * d) + 4.0 * S * S * d
 

@@ -77,30 +77,19 @@ KERNEL_KNOBS = {"main256": "256", "main128": "128", "main64": "64", "main32": "3
                 "skinny32": "s32"}
 
 
-@pytest.fixture
-def tile_knob():
-    import os
-    old = os.environ.get("SQ8_TILE")
-    yield os.environ
-    if old is None:
-        os.environ.pop("SQ8_TILE", None)
-    else:
-        os.environ["SQ8_TILE"] = old
-
-
 @pytest.mark.parametrize("shape", [(1, 64, 64), (33, 320, 200), (130, 3072, 520), (300, 1024, 1000)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_every_kernel_on_the_fp32_route(gemm, orc, tile_knob, shape):
+def test_every_kernel_on_the_fp32_route(gemm, orc, tile_gemm, shape):
     m, k, n = shape
     x, q, s, b = f32_problem(orc, m, k, n, False, 600 + n)
     pk = gemm.pack(weight_tensor(q, False, "kn"), layout="kn")
     wnk = weight_tensor(q, False, "nk")
     for name, knob in KERNEL_KNOBS.items():
-        tile_knob["SQ8_TILE"] = knob
-        y = gemm.product(dev(x), pk, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=torch.float32,
+        g = tile_gemm(knob)
+        y = g.product(dev(x), pk, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=torch.float32,
                          rounding=False)
-        d = gemm.product(dev(x), wnk, dev(s), layout="nk", bias=dev(b), epilogue="gelu_tanh",
-                         out_dtype=torch.float32, rounding=False)
+        d = g.product(dev(x), wnk, dev(s), layout="nk", bias=dev(b), epilogue="gelu_tanh",
+                      out_dtype=torch.float32, rounding=False)
         torch.cuda.synchronize()
         assert torch.equal(y, d), name  # one kernel, one K order: packed and [N, K] give the same bits
         judge(orc, y.cpu().numpy(), x, q, False, s, b, "gelu", torch.float32)

@@ -363,28 +363,16 @@ KERNEL_SHAPES = [
 ]
 
 
-@pytest.fixture
-def tile_knob():
-    import os
-    old = os.environ.get("SQ8_TILE")
-    yield os.environ
-    if old is None:
-        os.environ.pop("SQ8_TILE", None)
-    else:
-        os.environ["SQ8_TILE"] = old
-
-
 @pytest.mark.parametrize("fp8", [False, True], ids=["int8", "fp8"])
 @pytest.mark.parametrize("shape", KERNEL_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_each_kernel_on_the_same_problem(gemm, orc, tile_knob, shape, fp8):
+def test_each_kernel_on_the_same_problem(gemm, orc, tile_gemm, shape, fp8):
     m, k, n = shape
     x, q, s, b = problem(orc, m, k, n, fp8, seed=900 + m + n)
     pk = gemm.pack(weight_tensor(q, fp8, "kn"), layout="kn", fp8=fp8 or None)
     results = {}
     for name, knob in TILES.items():
-        tile_knob["SQ8_TILE"] = knob
         for out in (torch.float32, torch.bfloat16):
-            y = gemm.product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=out)
+            y = tile_gemm(knob).product(bf16_dev(x), pk, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=out)
             torch.cuda.synchronize()
             judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, "gelu", out)
             results[(name, out)] = y
@@ -394,8 +382,8 @@ def test_each_kernel_on_the_same_problem(gemm, orc, tile_knob, shape, fp8):
 
 
 @pytest.mark.parametrize("epi", ["silu", "situ"])
-def test_skinny_glu_and_qkv(gemm, orc, tile_knob, epi):
-    tile_knob["SQ8_TILE"] = "s64"
+def test_skinny_glu_and_qkv(orc, tile_gemm, epi):
+    gemm = tile_gemm("s64")
     m, k, n = 77, 640, 264  # GLU: 132 outputs, ragged against 32-column slabs
     x, q, s, b = problem(orc, m, k, n, False, seed=41)
     pk = gemm.pack(weight_tensor(q, False, "kn"), layout="kn", glu=True)
@@ -463,7 +451,7 @@ def test_residual_product_is_product_then_residual(gemm, orc, m, layout, gated):
 
 @pytest.mark.parametrize("m,n,epi,out_dtype", [(1000, 3000, "gelu", torch.bfloat16), (333, 1536, "none", torch.float32),
                                                (512, 2048, "silu", torch.bfloat16)])
-def test_tile_heights_same_bits(gemm, orc, monkeypatch, m, n, epi, out_dtype):
+def test_tile_heights_same_bits(gemm, orc, tile_gemm, m, n, epi, out_dtype):
     """The weight-direct kernel in 128-, 64- and 32-row tiles (the product's choice by how many tiles
     fill the CUs): every output the same bits whichever height computes it — each sum runs the same
     MFMA sequence over K — on ragged shapes, and within the bars of the truth on sampled rows."""
@@ -472,12 +460,10 @@ def test_tile_heights_same_bits(gemm, orc, monkeypatch, m, n, epi, out_dtype):
     wp = gemm.pack(weight_tensor(q, False, "nk"), layout="nk", glu=epi == "silu")
     outs = {}
     for tile in ("128", "64", "32"):
-        monkeypatch.setenv("SQ8_TILE", tile)
-        y = gemm.product(bf16_dev(x), wp, dev(s), bias=dev(b), out_dtype=out_dtype,
+        y = tile_gemm(tile).product(bf16_dev(x), wp, dev(s), bias=dev(b), out_dtype=out_dtype,
                          epilogue={"gelu": "gelu_tanh", "none": None, "silu": "silu_glu"}[epi])
         torch.cuda.synchronize()
         outs[tile] = y.float().cpu().numpy()
-    monkeypatch.delenv("SQ8_TILE")
     assert bitwise_equal(outs["64"], outs["128"]) == 0 and bitwise_equal(outs["32"], outs["128"]) == 0
     judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
 

@@ -134,3 +134,26 @@ def test_gguf_q8_0_weight_staged(gemm, orc, tmp_path):
     from refgen import bitwise_equal
     assert bitwise_equal(got.cpu().numpy(), want.cpu().numpy()) == 0
     judge_blocks(orc, got.cpu().numpy(), x, q, d, 32, b, "none", torch.float32)
+
+
+@pytest.mark.parametrize("cols", [192, 200])
+def test_submit_first_columns_on_block_scales(gemm, orc, cols):
+    """`submit(…columns:)` on a block-scaled [K, N] weight (the reference's Q8_0 submit dispatches
+    ⌈columns/64⌉ threadgroups on the whole weight's scales, TensorGEMM.swift:292-318): the first `columns`
+    of C written, the others untouched; each column the same bits as the whole product's (the codes and
+    their [K/B, N] scales read with the whole weight's stride); within the bars of the truth."""
+    m, k, n, block = 130, 512, 320, 32
+    x, q, d, b = q8_problem(orc, m, k, n, block, 71)
+    a = bf16_dev(x)
+    w = dev(np.ascontiguousarray(q.T)).view(torch.int8)                 # [K, N]
+    s = dev(np.ascontiguousarray(d.T).astype(np.float32))               # [K/B, N] fp32
+    whole = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    gemm.linear(a, int8=w, scales=s, per_column=True, c=whole, m=m, k=k, n=n, block=block, bias=dev(b),
+                epilogue="gelu_tanh")
+    part = torch.full((m, n), 7.0, dtype=torch.float32, device=DEV)
+    gemm.submit(a, int8=w, scales=s, per_column=True, c=part, m=m, k=k, n=n, columns=cols, block=block, bias=dev(b),
+                epilogue="gelu_tanh")
+    gemm.synchronize()
+    assert (part[:, cols:] == 7.0).all()
+    assert torch.equal(part[:, :cols], whole[:, :cols])
+    judge_blocks(orc, part[:, :cols].cpu().numpy(), x, q[:cols], d[:cols], block, b[:cols], "gelu", torch.float32)

@@ -17,14 +17,10 @@ from test_gpu_parity import DEV, bf16_dev, dev, judge, problem, weight_tensor
 pytestmark = pytest.mark.gpu
 
 
-def product(gemm, monkeypatch, tile, x, w, s, b, layout, epi, out_dtype=torch.bfloat16):
-    monkeypatch.setenv("SQ8_TILE", tile)
-    try:
-        y = gemm.product(bf16_dev(x), w, dev(s), layout=layout, bias=None if b is None else dev(b),
-                         epilogue="gelu_tanh" if epi == "gelu" else None, out_dtype=out_dtype)
-        torch.cuda.synchronize()
-    finally:
-        monkeypatch.delenv("SQ8_TILE")
+def product(tile_gemm, tile, x, w, s, b, layout, epi, out_dtype=torch.bfloat16):
+    y = tile_gemm(tile).product(bf16_dev(x), w, dev(s), layout=layout, bias=None if b is None else dev(b),
+                                epilogue="gelu_tanh" if epi == "gelu" else None, out_dtype=out_dtype)
+    torch.cuda.synchronize()
     return y.float().cpu().numpy()
 
 
@@ -35,33 +31,33 @@ def product(gemm, monkeypatch, tile, x, w, s, b, layout, epi, out_dtype=torch.bf
     (256, 2048, 768, True, "nk", "gelu", True, True),           # fp8 in place, one scale for the tensor
     (1, 512, 512, False, "packed", "gelu", True, False),        # one row
 ])
-def test_w256_same_bits_as_128(gemm, orc, monkeypatch, m, k, n, fp8, layout, epi, bias, tensor_scale):
+def test_w256_same_bits_as_128(gemm, orc, tile_gemm, m, k, n, fp8, layout, epi, bias, tensor_scale):
     x, q, s, b = problem(orc, m, k, n, fp8, 400 + m + n, bias=bias)
     if tensor_scale:
         s = np.array([float(np.median(s))], dtype=np.float32)
     w = weight_tensor(q, fp8, "nk")
     if layout == "packed":
         w = gemm.pack(w, layout="nk")
-    y256 = product(gemm, monkeypatch, "256", x, w, s, b, "nk", epi)
-    y128 = product(gemm, monkeypatch, "128", x, w, s, b, "nk", epi)
+    y256 = product(tile_gemm, "256", x, w, s, b, "nk", epi)
+    y128 = product(tile_gemm, "128", x, w, s, b, "nk", epi)
     assert bitwise_equal(y256, y128) == 0
     sj = np.full(n, s[0], dtype=np.float32) if tensor_scale else s
     judge(orc, y256, x, q, fp8, sj, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
 
 
-def test_w256_fp32_output_takes_128(gemm, orc, monkeypatch):
+def test_w256_fp32_output_takes_128(gemm, orc, tile_gemm):
     """An fp32 output is not the 256 kernel's: the product falls back to 128-row tiles, same bits."""
     m, k, n = 600, 512, 768
     x, q, s, b = problem(orc, m, k, n, False, 91)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
-    y256 = product(gemm, monkeypatch, "256", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
-    y128 = product(gemm, monkeypatch, "128", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
+    y256 = product(tile_gemm, "256", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
+    y128 = product(tile_gemm, "128", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
     assert bitwise_equal(y256, y128) == 0
     judge(orc, y256, x, q, False, s, b, "gelu", torch.float32, rows=orc.sample_rows(m, 64))
 
 
 @pytest.mark.parametrize("head_dim", [0, 128, 64])
-def test_w256_qkv(gemm, orc, monkeypatch, head_dim):
+def test_w256_qkv(gemm, orc, tile_gemm, head_dim):
     """The fused QKV product on 256-row tiles: each 64-column slab lies in one output and one head, its
     rows stored row-major or head-major; the same bits as the 128-row tiles, each third judged."""
     m, k, d = 700, 512, 384
@@ -69,12 +65,8 @@ def test_w256_qkv(gemm, orc, monkeypatch, head_dim):
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     outs = {}
     for tile in ("256", "128"):
-        monkeypatch.setenv("SQ8_TILE", tile)
-        try:
-            qq, kk, vv = gemm.product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
-            torch.cuda.synchronize()
-        finally:
-            monkeypatch.delenv("SQ8_TILE")
+        qq, kk, vv = tile_gemm(tile).product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
+        torch.cuda.synchronize()
         parts = []
         for t in (qq, kk, vv):
             t = t.float()
@@ -98,3 +90,25 @@ def test_slab_epilogue_same_bits_as_block_epilogue(gemm, orc):
     torch.cuda.synchronize()
     assert bitwise_equal(lean.float().cpu().numpy(), block.float().cpu().numpy()) == 0
     judge(orc, lean.float().cpu().numpy(), x, q, False, s, b, "gelu", torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+@pytest.mark.parametrize("blocks", [False, True], ids=["per_column", "q8_0"])
+def test_strided_fp32_operand_rounded_in_one_pass(gemm, orc, blocks):
+    """An fp32 A whose rows are further apart than k (lda > k) is rounded to bf16 by one strided pass: the
+    product equals the product on the same rows made contiguous, bit for bit (per-column and Q8_0 scales)."""
+    m, k, n = 300, 512, 640
+    wide = orc.normal_f32(61, (m, k + 40))
+    x = wide[:, :k]
+    q = orc.uniform_i8(62, (n, k)).view(np.uint8)
+    if blocks:
+        d = orc.uniform_f32(63, (n, k // 32), 1e-3, 2e-2).astype(np.float16)
+        w = weight_tensor(q, False, "nk")
+        strided = gemm.product_blocks(dev(wide)[:, :k], w, dev(d), 32, layout="nk")
+        packed = gemm.product_blocks(dev(np.ascontiguousarray(x)), w, dev(d), 32, layout="nk")
+    else:
+        s = orc.uniform_f32(63, (n,), 1e-3, 2e-2)
+        w = weight_tensor(q, False, "nk")
+        strided = gemm.product(dev(wide)[:, :k], w, dev(s), layout="nk")
+        packed = gemm.product(dev(np.ascontiguousarray(x)), w, dev(s), layout="nk")
+    torch.cuda.synchronize()
+    assert bitwise_equal(strided.float().cpu().numpy(), packed.float().cpu().numpy()) == 0
