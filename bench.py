@@ -22,6 +22,7 @@ the GPU box and scaled to the whole step.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -244,18 +245,23 @@ def c4_measure(route: str, steps: int, warmup: int, settle_ms: float) -> dict:
     # gets its own copy of x, made before the timed region; the settle and warm-up forwards reuse one.
     streams = [x.clone() for _ in range(steps)]
     work = x.clone()
+    gc.collect()
     st = settle(lambda: blk.forward_(work, temb), settle_ms)
     for _ in range(warmup):
         blk.forward_(work, temb)
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    t0 = time.perf_counter()
-    ev[0].record()
-    for i in range(steps):
-        blk.forward_(streams[i], temb)
-        ev[i + 1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    gc.disable()  # no collector pause while the timed forwards are queued
+    try:
+        t0 = time.perf_counter()
+        ev[0].record()
+        for i in range(steps):
+            blk.forward_(streams[i], temb)
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        gc.enable()
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
     mean = ev[0].elapsed_time(ev[steps]) / steps
     # The median forward: a host-side stall between two launches (the GPU then idles until the next one
@@ -427,10 +433,12 @@ def main() -> int:
         def step():
             ctx.product(xd, wd, sd, layout=lay, bias=bd, epilogue=epi, out=out)
 
+    gc.collect()
     settled = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    gc.disable()  # no collector pause while the timed steps are queued (enabled again below)
     # Every timed step is bracketed by HIP events on torch's current stream, the stream the context
     # launches on: ev[i] before step i, ev[steps] after the last (rotated workloads: three marks a step,
     # around the activation pass and the product).
@@ -446,6 +454,7 @@ def main() -> int:
         ev[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    gc.enable()
     step_ms = ev[0].elapsed_time(ev[args.steps]) / args.steps
     per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
     kernel_ms = step_ms

@@ -147,17 +147,18 @@ class TensorGEMM:
 
     def linear(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
                c: torch.Tensor, m: int, k: int, n: int, weight_offset: int = 0, scales_offset: int = 0,
-               block: Optional[int] = None, rotation=None, rounding: bool = True, quantizing=None,
+               block: Optional[int] = None, rotation=None, rounding=None, quantizing=None,
                prequantized=None, settled: bool = False, layout: str = "kn", bias: Optional[torch.Tensor] = None,
                epilogue=None, fp8: Optional[bool] = None, columns: Optional[int] = None) -> float:
         """`linear(a:int8:weightOffset:scales:scalesOffset:perColumn:…:c:m:k:n:settled:)`
         (TensorGEMM.swift:264-290): C[m, n] = A[m, k] · (q · s), q `[k, n]` (`layout="kn"`, the
         map's) at `weight_offset` bytes into `int8`, its fp32 scales at `scales_offset` bytes into
         `scales` (`n` of them, or one: `per_column` False). `a` fp32 is rounded to bf16 first when
-        `rounding` (the `rounding:` scratch route, TensorGEMMBF16.swift:208-264), or with `rounding`
-        False taken whole (the fp32 route, sq8_linear_f32: each value split exactly into three bf16
-        parts, K tripled; rotated in fp32 first with a `rotation`; block scales too); `a` bf16 is
-        already rounded. `rotation`: a convrot weight's group (an int, or the reference's
+        `rounding` is given — True or the reference's `(buffer, offset, rows)`, whose scratch this
+        library replaces with its own (the `rounding:` route, TensorGEMMBF16.swift:208-264) — and
+        otherwise, as the reference's default `rounding: nil`, taken whole (the fp32 route,
+        sq8_linear_f32: each value split exactly into three bf16 parts, K tripled; rotated in fp32 first
+        with a `rotation`; block scales too); `a` bf16 is already rounded. `rotation`: a convrot weight's group (an int, or the reference's
         `(group, scratch, offset, chunk)`, whose scratch and chunk this library replaces with its
         own), the activation rotated by it first (TensorGEMMBF16.swift:222-233). Returns the GPU
         seconds, 0 when `settled` (queued).
@@ -262,7 +263,7 @@ class TensorGEMM:
 
     def submit(self, a: torch.Tensor, *, int8: torch.Tensor, scales: torch.Tensor, per_column: bool,
                c: torch.Tensor, m: int, k: int, n: int, columns: int, weight_offset: int = 0, scales_offset: int = 0,
-               block: Optional[int] = None, rotation=None, rounding: bool = True, layout: str = "kn",
+               block: Optional[int] = None, rotation=None, rounding=None, layout: str = "kn",
                bias: Optional[torch.Tensor] = None, epilogue=None, fp8: Optional[bool] = None) -> None:
         """`submit(a:int8:…:c:m:k:n:columns:)` (TensorGEMM.swift:292-360): the product on the first
         `columns` of C only, queued and not waited for — the caller computes the other columns

@@ -224,14 +224,15 @@ def test_rotated_product_matches_the_widened_route(gemm, orc):
 
 
 def test_linear_mirror_takes_the_rotation(gemm, orc):
-    # TensorGEMM.linear(…rotation:…) with the reference's (group, scratch, offset, chunk) tuple.
+    # TensorGEMM.linear(…rotation:…rounding:…) with the reference's (group, scratch, offset, chunk) and
+    # (buffer, offset, rows) tuples: the rotated activation rounded to bf16, then the product.
     m, k, n = 70, 512, 96
     x = orc.normal_f32(21, (m, k))
     q_kn = orc.uniform_i8(22, (k, n))
     s = orc.uniform_f32(23, (n,), 1e-3, 2e-2)
     c = torch.empty((m, n), dtype=torch.float32, device=DEV)
     secs = gemm.linear(dev(x), int8=dev(q_kn).view(torch.int8), scales=dev(s), per_column=True, c=c, m=m, k=k, n=n,
-                       rotation=(256, None, 0, 64))
+                       rotation=(256, None, 0, 64), rounding=(None, 0, 64))
     assert secs > 0
     xr = orc.f32_to_bf16(orc.rotate_groups(x, 256))
     plain = gemm.product(bf16_dev(xr), dev(q_kn).view(torch.int8), dev(s), layout="kn", out_dtype=torch.float32)
