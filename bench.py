@@ -38,8 +38,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
 RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a
 # 512 MiB copy), by (workload, weight layout), as measured by the rocprofv3 --pmc runs recorded in
-# profiles/gemm_wd_kernel_c1_up_int8_packed_gelu.md.
-TRAFFIC_BYTES = {("c1_up", "packed"): 543.4e6}
+# profiles/ (gemm_w256_kernel_c1_up_int8_packed_gelu.md, short_m_skinny_kernel_and_short_tiles.md).
+TRAFFIC_BYTES = {("c1_up", "packed"): 403.6e6, ("c2_skinny", "packed"): 47.47e6, ("c0", "packed"): 56.95e6,
+                 ("skinny_m1", "packed"): 9.70e6, ("skinny_m16", "packed"): 10.53e6, ("skinny_m64", "packed"): 13.19e6}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
 # name: M, K, N, weight type, epilogue, activation distribution, description.
@@ -54,6 +55,10 @@ WORKLOADS = {
                "C2 fused QKV (4096 image + 512 text tokens): int8 weight [9216, 3072], bias, Q/K/V [4608, 3072] bf16"),
     "c2_skinny": (512, 3072, 3072, "int8", None, "normal",
                   "C2 skinny text stream: int8 weight [3072, 3072], bias, bf16 out"),
+    # Short rows on C2's text-stream weight (3072 x 3072): the bandwidth-bound end of the skinny path.
+    "skinny_m1": (1, 3072, 3072, "int8", None, "normal", "one row on an int8 weight [3072, 3072], bias, bf16 out"),
+    "skinny_m16": (16, 3072, 3072, "int8", None, "normal", "16 rows on an int8 weight [3072, 3072], bias, bf16 out"),
+    "skinny_m64": (64, 3072, 3072, "int8", None, "normal", "64 rows on an int8 weight [3072, 3072], bias, bf16 out"),
     "c3_gate_up": (4096, 3840, 20480, "fp8", "silu_glu", "normal",
                    "C3 fp8-e4m3 gate+up fused (2 x 10240) with SiLU-GLU, bf16 out [4096, 10240]"),
     "c3_down": (4096, 10240, 3840, "fp8", None, "silu",
