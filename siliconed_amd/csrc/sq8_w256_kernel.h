@@ -104,13 +104,13 @@ gemm_w256_kernel(const GemmArgs p) {
     u32x4 raw[4][4];  // [K step mod 4][load j]
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
-        const kern::gbytes base = Wg + (uint32_t)min(t, KT - 1) * w_step;
+        const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
 #pragma unroll
         for (int j = 0; j < 4; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
     };
     auto issue_w1 = [&](int t, auto buf, auto jc) {
         constexpr int B = decltype(buf)::value, J = decltype(jc)::value;
-        const kern::gbytes base = Wg + (uint32_t)min(t, KT - 1) * w_step;
+        const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
         raw[B][J] = kern::gld<u32x4>(base, w_off[J]);
     };
 
@@ -250,11 +250,11 @@ gemm_w256_kernel(const GemmArgs p) {
 }
 
 // True when the 256 × 256 kernel runs this product: bf16 output, a plain or GELU epilogue, whole
-// 64-column slabs that each lie in one output (and one head), 16-byte stores and scale/bias loads,
-// the activation's own K steps (not the fp32 route's parts).
+// 64-column slabs that each lie in one output (and one head), 16-byte stores and scale/bias loads. The
+// fp32 route's three parts along K (kt_w > 0) face the weight's steps in turn (weight_step).
 inline bool w256_fits(const GemmArgs &p, int epi, int out) {
     return (epi == EPI_NONE || epi == EPI_GELU) && out == OUT_BF16 && p.glu_half == 0 && p.N % 64 == 0 &&
-           p.split % 64 == 0 && p.head_dim % 64 == 0 && p.c_vec16 && p.sb_vec && p.kt_w == 0;
+           p.split % 64 == 0 && p.head_dim % 64 == 0 && p.c_vec16 && p.sb_vec;
 }
 
 template <int WT, int WL>

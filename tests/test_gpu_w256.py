@@ -112,3 +112,22 @@ def test_strided_fp32_operand_rounded_in_one_pass(gemm, orc, blocks):
         packed = gemm.product(dev(np.ascontiguousarray(x)), w, dev(s), layout="nk")
     torch.cuda.synchronize()
     assert bitwise_equal(strided.float().cpu().numpy(), packed.float().cpu().numpy()) == 0
+
+
+def test_w256_on_the_fp32_route(gemm, orc, tile_gemm):
+    """The fp32 route (an fp32 activation used whole: three exact bf16 parts along K, each facing the whole
+    weight) on 256-row tiles, bf16 out: the same bits as the 128-row tiles, judged against the fp64 truth
+    of the fp32 activation."""
+    m, k, n = 520, 1024, 768
+    x = orc.normal_f32(81, (m, k))
+    q = orc.uniform_i8(82, (n, k)).view(np.uint8)
+    s = orc.uniform_f32(83, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(84, (n,), 0.0, 0.02)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    outs = {}
+    for tile in ("256", "128"):
+        y = tile_gemm(tile).product(dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh", rounding=False)
+        torch.cuda.synchronize()
+        outs[tile] = y.float().cpu().numpy()
+    assert bitwise_equal(outs["256"], outs["128"]) == 0
+    judge(orc, outs["256"], x, q, False, s, b, "gelu", torch.bfloat16, rows=orc.sample_rows(m, 64))
