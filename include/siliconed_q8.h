@@ -82,11 +82,13 @@ typedef struct sq8_ctx sq8_ctx;
 
 /* Creates a context on HIP device `device`, launching on `stream` (a hipStream_t; NULL = the
  * device's null stream). Refuses (SQ8_ENODEVICE) a device that is not gfx950.
- * Two measurement knobs are read from the environment here, once per context: SQ8_TILE ("256",
- * "128", "64", "32", "s64", "s32": the weight-direct kernels' tile) and SQ8_Q8_TILE ("256", "512",
- * "128x256", "128x128": the block-scale kernel's tile). A context created with one set runs every
- * product of that family on that tile (a tile that cannot serve a product falls back to the nearest
- * one that can); unset, the library chooses per product.
+ * Three measurement knobs are read from the environment here, once per context: SQ8_TILE ("256",
+ * "128", "64", "32", "s64", "s32": the weight-direct kernels' tile), SQ8_Q8_TILE ("256", "512",
+ * "128x256", "128x128": the block-scale kernel's tile) and SQ8_SPLITS (a count ≥ 1: the skinny
+ * kernel's K split over workgroups, added by a second launch; 1, the default, none; at most the
+ * product's K steps). A context created with
+ * one set runs every product of that family on that tile (a tile that cannot serve a product falls
+ * back to the nearest one that can); unset, the library chooses per product.
  * Replaces: TensorGEMM.init?(device:queue:roundingActivations:quantizingActivations:)
  * (Sources/Siliconed/TensorGEMM.swift:206-232). */
 int sq8_create(int device, void *stream, sq8_ctx **out);
@@ -114,9 +116,10 @@ int sq8_supports(const sq8_ctx *ctx, int a_dtype, int w_dtype, int w_layout, int
  * `ldw`/`ldc` say so (the `columns` argument of `submit`, TensorGEMM.swift:296).
  * `gpu_seconds`: NULL → the launch is queued and the call returns at once (`settled`,
  * TensorGEMM.swift:261-263); non-NULL → the call waits and writes the kernel's GPU seconds
- * (TensorGEMM.swift:268-272, `Attention.verdict`). One exception to "at once": the context's two
- * growable buffers — the bf16 copy (or, on the fp32 route, the three parts) of an fp32 A, and the
- * repack of [K, N] codes read in place — are sized by the largest product so far; a call that needs
+ * (TensorGEMM.swift:268-272, `Attention.verdict`). One exception to "at once": the context's
+ * growable buffers — the bf16 copy (or, on the fp32 route, the three parts) of an fp32 A, the
+ * repack of [K, N] codes read in place, and the fp32 partial sums of a short product whose K steps
+ * are split over several workgroups (added by a second launch) — are sized by the largest product so far; a call that needs
  * more first synchronizes the context's stream (queued work may still read the old buffer), frees
  * and allocates. A caller that must never block runs one product of its largest shape first.
  * Replaces: TensorGEMM.linear(a:int8:weightOffset:scales:scalesOffset:perColumn:block:rotation:

@@ -30,9 +30,12 @@ struct sq8_ctx {
     size_t scratch_bytes;
     void *wpack;            // [K, N] codes repacked for the weight-direct kernels, per product
     size_t wpack_bytes;
+    void *part;             // the skinny kernel's partial sums of a K split
+    size_t part_bytes;
     rocblas_handle blas;    // the bf16-weight product's library GEMM (created on its first call)
-    int wd_tile;            // measurement knobs, read once at sq8_create (SQ8_TILE, SQ8_Q8_TILE): a forced
-    int q8_tile;            // weight-direct / block-scale tile, or -1 (the product's own choice)
+    int wd_tile;            // measurement knobs, read once at sq8_create (SQ8_TILE, SQ8_Q8_TILE, SQ8_SPLITS): a
+    int q8_tile;            // forced weight-direct / block-scale tile, or -1 (the product's own choice); the
+    int splits;             // skinny kernel's K split count (1: none, the default)
 };
 
 namespace {
@@ -316,6 +319,21 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
         const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
+        if ((tile == sq8::WD_SKINNY32 || tile == sq8::WD_SKINNY64) && ctx->splits > 1) {
+            // Short M with the SQ8_SPLITS knob: the K steps split over several workgroups per tile, partial
+            // sums in the context's buffer, added in split order by a second launch. Not the default: the
+            // second launch's fixed cost (~3.4 µs on this chip) exceeds what the split saves (M = 1 at
+            // K = N = 3072: 7.5 µs unsplit, 5.0 + 4.5 in four splits).
+            const int splits = std::min(ctx->splits, p.kt);
+            if (splits > 1) {
+                const int64_t bytes = sq8::skinny_part_bytes(q.m, q.n, is_glu(q.epilogue),
+                                                             tile == sq8::WD_SKINNY32 ? 32 : 64, splits);
+                st = reserve_buffer(ctx, &ctx->part, &ctx->part_bytes, (size_t)bytes);
+                if (st != SQ8_OK) return st;
+                p.part = static_cast<float *>(ctx->part);
+                p.splits = splits;
+            }
+        }
         e = sq8::launch_wdirect(p, tile, wt, wl, epi, out, ctx->stream);
     } else if (q.residual || q.exact) {
         return SQ8_EUNSUPPORTED;  // the residual epilogue and the fp32 route run on the weight-direct kernels only
@@ -714,6 +732,8 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
                                              {"32", sq8::WD_32}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32}});
     ctx->q8_tile = knob(getenv("SQ8_Q8_TILE"), {{"256", sq8::BL_64x256}, {"512", sq8::BL_64x512},
                                                 {"128x256", sq8::BL_128x256}, {"128x128", sq8::BL_128x128}});
+    const char *splits = getenv("SQ8_SPLITS");
+    ctx->splits = splits && atoi(splits) >= 1 ? atoi(splits) : 1;
     uint8_t *unused = nullptr;
     (void)static_scratch_of(device, &unused);  // set-up; sq8_linear_quantized_static retries and reports
     e = hipEventCreate(&ctx->begin);
@@ -735,6 +755,7 @@ int sq8_destroy(sq8_ctx *ctx) {
     if (e != hipSuccess) st = hip_status(e);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->wpack) (void)hipFree(ctx->wpack);
+    if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->blas) (void)rocblas_destroy_handle(ctx->blas);
     (void)hipEventDestroy(ctx->begin);
     (void)hipEventDestroy(ctx->end);

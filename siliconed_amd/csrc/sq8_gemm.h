@@ -33,6 +33,9 @@ struct GemmArgs {
     const float *sx;        // W8A8: the activation's row scales fp32 [M] (`a` then holds int8 codes)
     int kt_w;               // W8A8: K steps of 64 of the packed weight; weight-direct kernels: the weight's
                             // K steps when the activation holds several parts along K (0: kt)
+    float *part;            // the skinny kernel's K split: fp32 partial sums, skinny_part_bytes() of them
+    int splits;             // > 1: the skinny kernel's K steps split over this many workgroups per tile, whose
+                            // sums a second launch adds in split order before the epilogue
 };
 
 enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };
@@ -54,6 +57,8 @@ enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 
 // product), else the tallest of 128, 64 and 32 rows whose tiles number at least 144 (enough to occupy
 // the 256 CUs), else the skinny kernel.
 int choose_wd_tile(int M, int N, bool glu);
+// Bytes of the partial sums of a split skinny product (tile height bm, `splits` splits).
+int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits);
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);
 
 // Bytes of the packed layout of a weight with k rows of K and n columns (GLU: n = 2h, packed in

@@ -38,6 +38,12 @@ int choose_wd_tile(int M, int N, bool glu) {
     return M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
 }
 
+int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits) {
+    const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
+    const long tiles = (long)((M + bm - 1) / bm) * slabs;
+    return (int64_t)splits * tiles * (2 * (bm / 32)) * 1024 * 4;
+}
+
 int choose_tile(int M, int N_out, bool glu) {
     // Tiles of 256 × 256 while they fill the 256 CUs at least 3/4 of the way; 128 × 128 below.
     const int n_virtual = glu ? 2 * N_out : N_out;

@@ -31,23 +31,36 @@ def gemm():
 
 
 @pytest.fixture(scope="session")
-def tile_gemm(gemm):
-    """knob → a context on cuda:0 created with SQ8_TILE = knob (the library reads its tile knobs once, when
-    a context is created): the product on that forced weight-direct tile. Contexts are kept per knob."""
+def knob_gemm(gemm):
+    """(tile, splits) → a context on cuda:0 created with SQ8_TILE = tile and SQ8_SPLITS = splits (None: unset;
+    the library reads its knobs once, when a context is created). Contexts are kept per pair."""
     import siliconed_amd as sq
     made = {}
 
-    def get(knob: str):
-        if knob not in made:
-            old = os.environ.get("SQ8_TILE")
-            os.environ["SQ8_TILE"] = knob
+    def get(tile=None, splits=None):
+        key = (tile, splits)
+        if key not in made:
+            env = {"SQ8_TILE": tile, "SQ8_SPLITS": None if splits is None else str(splits)}
+            old = {name: os.environ.get(name) for name in env}
             try:
-                made[knob] = sq.TensorGEMM.make(0)
+                for name, value in env.items():
+                    if value is None:
+                        os.environ.pop(name, None)
+                    else:
+                        os.environ[name] = value
+                made[key] = sq.TensorGEMM.make(0)
             finally:
-                if old is None:
-                    os.environ.pop("SQ8_TILE", None)
-                else:
-                    os.environ["SQ8_TILE"] = old
-        return made[knob]
+                for name, value in old.items():
+                    if value is None:
+                        os.environ.pop(name, None)
+                    else:
+                        os.environ[name] = value
+        return made[key]
 
     return get
+
+
+@pytest.fixture(scope="session")
+def tile_gemm(knob_gemm):
+    """knob → a context on cuda:0 created with SQ8_TILE = knob: the product on that forced weight-direct tile."""
+    return lambda knob: knob_gemm(knob, None)

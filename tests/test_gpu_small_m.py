@@ -39,7 +39,10 @@ def _bound_check(orc, got, xt, wv, s, b, epi, out_dtype, k_eff):
     e = eps * mag
     ulp = 2.0 ** -7 if out_dtype == torch.bfloat16 else 2.0 ** -23
     tiny = 2.0 ** -126
-    if epi == "gelu":
+    if epi == "none":
+        f = pre
+        bound = e + ulp * np.abs(f) + tiny
+    elif epi == "gelu":
         f = orc.exact_rows(rows, xt, wv, False, k, n, scale=s, bias=b, epilogue=orc.EPI_GELU_TANH)
         bound = 1.13 * e + (2.0 ** -18 + ulp) * np.abs(f) + tiny
     else:
