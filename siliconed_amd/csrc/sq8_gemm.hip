@@ -30,8 +30,10 @@ int choose_wd_tile(int M, int N, bool glu) {
     const long tn = (slabs + 3) / 4;
     auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * (bm == 256 ? (slabs + 3) / 4 : tn); };
     // 256 × 256 tiles (one workgroup a CU) from two rounds of them on 256 CUs: C1's up-projection,
-    // 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians).
-    if (!glu && tiles(256) / 2 >= 256) return WD_256;
+    // 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians); C3's fp8 gate-up
+    // (SiLU-GLU, 1280 tiles) 1353 against 1290 TFLOP/s. One round or less (C4's Wo and W_down, 216
+    // tiles) runs faster in 128-row tiles.
+    if (tiles(256) / 2 >= 256) return WD_256;
     if (tiles(128) >= 144) return WD_128;
     if (tiles(64) >= 144) return WD_64;
     if (tiles(32) >= 144) return WD_32;

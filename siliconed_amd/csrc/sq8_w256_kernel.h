@@ -25,8 +25,10 @@
 // 16 MFMAs; at the end: wait until step s+2's loads have landed (12 younger loads may fly), barrier.
 //
 // The tile's scales and biases are fetched into LDS by direct loads at the start (they land with
-// the prologue); the epilogue reads them there. Epilogue: bf16 out, bias and GELU or none, written
-// through the wave's LDS region as full 128-byte row segments (slab_epilogue_bf16).
+// the prologue); the epilogue reads them there. Epilogue: bf16 out with no activation or GELU through the
+// wave's LDS region as full 128-byte row segments (slab_epilogue_bf16); the GLU epilogues (a slab is then
+// 32 columns of each half: the packed GLU layout), fp32 outputs and the gated residual 32 × 32 block by
+// block (store_block).
 #pragma once
 
 #include "sq8_wdirect_kernel.h"
@@ -34,10 +36,12 @@
 namespace sq8 {
 namespace wd {
 
-template <int WT, int WL, int EPI>
+template <int WT, int WL, int EPI, int OUT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 gemm_w256_kernel(const GemmArgs p) {
-    static_assert(EPI == EPI_NONE || EPI == EPI_GELU, "plain or GELU epilogues");
+    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
+    constexpr bool SLAB = (EPI == EPI_NONE || EPI == EPI_GELU) && OUT == OUT_BF16;
+    static_assert(EPI != EPI_RESIDUAL || OUT == OUT_F32, "the residual stream is fp32");
     constexpr int BM = 256, NW = 4, FM = 8, NAS = 4;
     constexpr int SA = BM * 128;             // bytes per activation stage
     constexpr int A_PER_WAVE = BM / 8 / NW;  // 1 KB direct loads per wave per step
@@ -59,12 +63,14 @@ gemm_w256_kernel(const GemmArgs p) {
     const kern::gbytes Wg = (kern::gbytes)p.w;
     const int KT = p.kt;
 
-    // Scales (wave 0) and biases (wave 1) of the tile's 256 columns, 16 bytes a lane, first in issue
-    // order so that the prologue's wait covers them. Columns past N read the last four (never used).
+    // Scales (wave 0) and biases (wave 1) of the tile's 256 weight columns, 16 bytes a lane, first in
+    // issue order so that the prologue's wait covers them (GLU: lanes 0–31 the first half's 128
+    // columns, lanes 32–63 the second half's). Columns past the end read the last four (never used).
     if (wave < 2) {
         const float *src = wave == 0 ? (p.scale_per_col ? p.scale : nullptr) : p.bias;
         if (src != nullptr) {
-            const int col = min(tn * 256 + lane * 4, p.N - 4);
+            const int col = GLU ? min(tn * 128 + (lane & 31) * 4, p.glu_half - 4) + (lane >> 5) * p.glu_half
+                                : min(tn * 256 + lane * 4, p.N - 4);
             __builtin_amdgcn_global_load_lds((glb_ptr)(src + col), (lds_ptr)(lds + SB_OFF + wave * 1024), 16, 0, 0);
         }
     }
@@ -99,7 +105,7 @@ gemm_w256_kernel(const GemmArgs p) {
 
     uint32_t w_off[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, false>(p, slab, j, lane);
+    for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, j, lane);
     const uint32_t w_step = WL == W_PACKED ? 4096 : BK;
     u32x4 raw[4][4];  // [K step mod 4][load j]
     auto issue_w = [&](int t, auto buf) {
@@ -227,15 +233,17 @@ gemm_w256_kernel(const GemmArgs p) {
     wait_vmcnt<0>();
     step_barrier();
 
-    const int col0 = slab * 64;
-    if (col0 >= p.N) return;  // a last tile's waves past the weight's columns
+    const int n_out = GLU ? p.glu_half : p.N;
+    const int col0 = GLU ? slab * 32 : slab * 64;
+    if (col0 >= n_out) return;  // a last tile's waves past the weight's columns
     const bool has_bias = p.bias != nullptr;
     ColParams cp[2];
     static_for<0, 2>([&](auto bc) {
         constexpr int b = decltype(bc)::value;
         static_for<0, 4>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
-            const int lc = wave * 64 + 32 * b + 8 * g + 4 * h;
+            // Block b's columns in the LDS copy (GLU: block b is half b's 32 columns of the slab).
+            const int lc = (GLU ? 128 * b + wave * 32 : wave * 64 + 32 * b) + 8 * g + 4 * h;
             const f32x4 sv = p.scale_per_col ? *reinterpret_cast<const f32x4 *>(lds + SB_OFF + lc * 4)
                                              : f32x4{p.scale[0], p.scale[0], p.scale[0], p.scale[0]};
             const f32x4 bv = has_bias ? *reinterpret_cast<const f32x4 *>(lds + SB_OFF + 1024 + lc * 4) : f32x4{0, 0, 0, 0};
@@ -246,29 +254,65 @@ gemm_w256_kernel(const GemmArgs p) {
             });
         });
     });
-    slab_epilogue_bf16<FM, EPI>(p, acc, cp, has_bias, m0, col0, lds + wave * (BM * 128), lane);
+    if constexpr (SLAB) {
+        slab_epilogue_bf16<FM, EPI>(p, acc, cp, has_bias, m0, col0, lds + wave * (BM * 128), lane);
+    } else {
+        constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);
+        uint8_t *region = lds + wave * REGION;
+        static_for<0, FM>([&](auto bmc) {
+            constexpr int bm = decltype(bmc)::value;
+            if constexpr (GLU) {
+                store_block<EPI, OUT>(p, acc[0][bm], cp[0], acc[1][bm], cp[1], has_bias, col0, m0 + 32 * bm, n_out,
+                                      region, lane);
+            } else {
+                static_for<0, 2>([&](auto bc) {
+                    constexpr int b = decltype(bc)::value;
+                    if (col0 + 32 * b < n_out)
+                        store_block<EPI, OUT>(p, acc[b][bm], cp[b], acc[b][bm], cp[b], has_bias, col0 + 32 * b, m0 + 32 * bm,
+                                              n_out, region, lane);
+                });
+            }
+        });
+    }
 }
 
-// True when the 256 × 256 kernel runs this product: bf16 output, a plain or GELU epilogue, whole
-// 64-column slabs that each lie in one output (and one head), 16-byte stores and scale/bias loads. The
-// fp32 route's three parts along K (kt_w > 0) face the weight's steps in turn (weight_step).
+// True when the 256 × 256 kernel runs this product: whole 64-column slabs (GLU: whole 32-column
+// slabs of each half) and 16-byte scale/bias loads; for the slab epilogue (bf16 out, no activation or
+// GELU) also slabs that each lie in one output (and one head) and 16-byte stores. The fp32 route's three
+// parts along K (kt_w > 0) face the weight's steps in turn (weight_step).
 inline bool w256_fits(const GemmArgs &p, int epi, int out) {
-    return (epi == EPI_NONE || epi == EPI_GELU) && out == OUT_BF16 && p.glu_half == 0 && p.N % 64 == 0 &&
-           p.split % 64 == 0 && p.head_dim % 64 == 0 && p.c_vec16 && p.sb_vec;
+    if (!p.sb_vec) return false;
+    if (p.glu_half > 0 ? p.glu_half % 32 != 0 : p.N % 64 != 0) return false;
+    if (epi == EPI_RESIDUAL && out != OUT_F32) return false;
+    if ((epi == EPI_NONE || epi == EPI_GELU) && out == OUT_BF16)
+        return p.split % 64 == 0 && p.head_dim % 64 == 0 && p.c_vec16;
+    return true;
 }
 
 template <int WT, int WL>
-hipError_t launch_w256(const GemmArgs &args, int epi, hipStream_t stream) {
+hipError_t launch_w256(const GemmArgs &args, int epi, int out, hipStream_t stream) {
     GemmArgs p = args;
+    const bool glu = epi == EPI_SILU_GLU || epi == EPI_SITU_GLU;
     p.tiles_m = (p.M + 255) / 256;
-    p.tiles_n = (p.N + 255) / 256;
+    p.tiles_n = glu ? (p.glu_half / 32 + 3) / 4 : (p.N + 255) / 256;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    if (epi == EPI_GELU)
-        hipLaunchKernelGGL((gemm_w256_kernel<WT, WL, EPI_GELU>), dim3(blocks), dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL((gemm_w256_kernel<WT, WL, EPI_NONE>), dim3(blocks), dim3(256), 0, stream, p);
-    return hipGetLastError();
+#define SQ8_CASE(E, O)                                                                                   \
+    if (epi == E && out == O) {                                                                          \
+        hipLaunchKernelGGL((gemm_w256_kernel<WT, WL, E, O>), dim3(blocks), dim3(256), 0, stream, p);  \
+        return hipGetLastError();                                                                        \
+    }
+    SQ8_CASE(EPI_NONE, OUT_BF16)
+    SQ8_CASE(EPI_GELU, OUT_BF16)
+    SQ8_CASE(EPI_NONE, OUT_F32)
+    SQ8_CASE(EPI_GELU, OUT_F32)
+    SQ8_CASE(EPI_SILU_GLU, OUT_BF16)
+    SQ8_CASE(EPI_SILU_GLU, OUT_F32)
+    SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
+    SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    SQ8_CASE(EPI_RESIDUAL, OUT_F32)
+#undef SQ8_CASE
+    return hipErrorInvalidValue;
 }
 
 }  // namespace wd

@@ -1,11 +1,12 @@
-"""The 256 × 256 kernel (one workgroup per CU) and the slab epilogue, on an MI355X.
+"""The 256 × 256 kernel (one workgroup per CU), its slab and block epilogues, on an MI355X.
 
 Every output of the weight-direct kernels is one MFMA sequence over K whatever the tile, and the slab
 epilogue applies the same scale, bias and activation as the 32 × 32-block one: so the 256-row tiles
 give the same bits as the 128-row tiles, and both are judged against the oracle's fp64 truth on
 sampled rows at the reference's bars (DiagnosticProbes.swift:75-82, DiagnosticJudgement.swift:39-71).
 Shapes cover a ragged last row tile, a last column tile with fewer slabs than waves, per-tensor scales,
-no bias, fp8 codes, both weight layouts, and the QKV split (row-major and head-major).
+no bias, fp8 codes, both weight layouts, the QKV split (row-major and head-major), the GLU epilogues,
+fp32 outputs and the gated residual.
 """
 import numpy as np
 import pytest
@@ -45,8 +46,9 @@ def test_w256_same_bits_as_128(gemm, orc, tile_gemm, m, k, n, fp8, layout, epi, 
     judge(orc, y256, x, q, fp8, sj, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
 
 
-def test_w256_fp32_output_takes_128(gemm, orc, tile_gemm):
-    """An fp32 output is not the 256 kernel's: the product falls back to 128-row tiles, same bits."""
+def test_w256_fp32_output(gemm, orc, tile_gemm):
+    """fp32 outputs on 256-row tiles (32 × 32 blocks through the epilogue regions): the same bits as the
+    128-row tiles."""
     m, k, n = 600, 512, 768
     x, q, s, b = problem(orc, m, k, n, False, 91)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
@@ -131,3 +133,47 @@ def test_w256_on_the_fp32_route(gemm, orc, tile_gemm):
         outs[tile] = y.float().cpu().numpy()
     assert bitwise_equal(outs["256"], outs["128"]) == 0
     judge(orc, outs["256"], x, q, False, s, b, "gelu", torch.bfloat16, rows=orc.sample_rows(m, 64))
+
+
+@pytest.mark.parametrize("epi,h,fp8,layout", [("silu", 640, False, "packed"), ("situ", 160, True, "nk"),
+                                              ("silu", 2048, True, "packed")])
+def test_w256_glu(gemm, orc, tile_gemm, epi, h, fp8, layout):
+    """The GLU epilogues on 256-row tiles (a slab: 32 columns of each half), bf16 and fp32 out: the same bits
+    as the 128-row tiles, judged against the fp64 truth. h = 160: five slabs, the last tile one slab."""
+    m, k = 600, 768
+    x, q, s, b = problem(orc, m, k, 2 * h, fp8, 500 + h)
+    w = weight_tensor(q, fp8, "nk")
+    if layout == "packed":
+        w = gemm.pack(w, layout="nk", glu=True)
+    name = {"silu": "silu_glu", "situ": "situ_glu"}[epi]
+    for out in (torch.bfloat16, torch.float32):
+        ys = {}
+        for tile in ("256", "128"):
+            y = tile_gemm(tile).product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), epilogue=name, out_dtype=out)
+            torch.cuda.synchronize()
+            ys[tile] = y.float().cpu().numpy()
+        assert bitwise_equal(ys["256"], ys["128"]) == 0
+        judge(orc, ys["256"], x, q, fp8, s, b, epi, out, rows=orc.sample_rows(m, 64))
+
+
+@pytest.mark.parametrize("gated", [True, False])
+def test_w256_residual(gemm, orc, tile_gemm, gated):
+    """x += gate ⊙ (s ⊙ (A·W) + b) on 256-row tiles: the same bits as on the 128-row tiles, and as the fp32
+    product followed by the gated residual pass."""
+    m, k, n = 700, 1024, 768
+    x_, q, s, b = problem(orc, m, k, n, False, 81 + gated)
+    stream = orc.normal_f32(83, (m, n), 0.0, 1.0)
+    gate = dev(orc.normal_f32(84, (n,), 0.0, 0.5)) if gated else None
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    outs = {}
+    for tile in ("256", "128"):
+        got = dev(stream)
+        tile_gemm(tile).product_residual(got, bf16_dev(x_), w, dev(s), bias=dev(b), gate=gate)
+        torch.cuda.synchronize()
+        outs[tile] = got.cpu().numpy()
+    assert bitwise_equal(outs["256"], outs["128"]) == 0
+    y = tile_gemm("256").product(bf16_dev(x_), w, dev(s), bias=dev(b), out_dtype=torch.float32)
+    expect = dev(stream)
+    gemm.gated_residual(expect, y, gate)
+    torch.cuda.synchronize()
+    assert bitwise_equal(outs["256"], expect.cpu().numpy()) == 0
