@@ -86,7 +86,7 @@ def test_refusals(tmp_path):
     _refused(str(p), "truncated", "shorter than a prologue")
     for v in (1, 4):
         path, _ = _raw(tmp_path, {"page": 64, "tensors": {}}, version=v, name=f"v{v}.silicon")
-        _refused(path, "bad_magic", "not a Siliconed map")
+        _refused(path, "bad_magic", "not a Siliconed map's signature")
     path, _ = _raw(tmp_path, {"page": 64, "tensors": {}}, length=10 ** 6, name="len.silicon")
     _refused(path, "truncated", "header length")
     path, _ = _raw(tmp_path, b"[1, 2]", name="notobj.silicon")
@@ -111,9 +111,9 @@ def test_refusals(tmp_path):
         ({"w": _entry(0, [4, 8], nbytes=64, scale={"offset": 24, "dtype": "float32", "shape": [8]})}, "bad_header",
          "does not fit"),
         ({"w": _entry(0, [4, 8], nbytes=64, scale={"offset": 32, "dtype": "int8", "shape": [8]})}, "bad_header",
-         "malformed scale"),
+         "scale record is malformed"),
         ({"w": _entry(0, [4, 8], dtype="float32", nbytes=128, scale={"offset": 32, "dtype": "float32", "shape": [8]})},
-         "bad_header", "malformed scale"),
+         "bad_header", "scale record is malformed"),
         ({"w": _entry(0, [4, 8], nbytes=64, scale={"offset": 32, "dtype": "float32", "shape": [8]},
                       rotation={"kind": "hadamard", "group": 4})}, "bad_header", "unknown"),
         ({"w": _entry(0, [4, 8], nbytes=64, scale={"offset": 32, "dtype": "float32", "shape": [8]},

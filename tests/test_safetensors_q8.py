@@ -48,7 +48,7 @@ def test_a_valid_file_reads(tmp_path):
 
 def test_hostile_headers_are_refused_by_name(tmp_path):
     for n in (0, 3, 8):
-        _refused(_file(tmp_path, f"short{n}.safetensors", b"\1" * n), "too short")
+        _refused(_file(tmp_path, f"short{n}.safetensors", b"\1" * n), "cannot hold a safetensors header")
     _refused(_st(tmp_path, "huge.safetensors", "{}", 0, length=2 ** 64 - 1), "length")
     _refused(_st(tmp_path, "past.safetensors", "{}", 0, length=3), "length")
     _refused(_st(tmp_path, "spec.safetensors", "{}", 0, length=100_000_001), "length")
@@ -177,7 +177,7 @@ def test_the_published_layouts_are_recognized(tmp_path):
     r = _recognized(tmp_path, "table.safetensors",
                     {**t, "b.attn.comfy_attention.config": _text({"attention": "comfy_kitchen_int8"})},
                     {"_quantization_metadata": json.dumps({"layers": {"w": {"format": "int8_tensorwise"}}})})
-    assert r.groups["w.weight"].format == "ComfyUI int8_tensorwise" and r.notes[0].startswith("1 ComfyUI attention")
+    assert r.groups["w.weight"].format == "ComfyUI int8_tensorwise" and r.notes[0].startswith("1 ComfyUI attention setting")
 
 
 def test_siliconed_sq8_is_read_and_its_lower_tiers_refused(tmp_path):
@@ -191,7 +191,7 @@ def test_siliconed_sq8_is_read_and_its_lower_tiers_refused(tmp_path):
     _refuses(tmp_path, "sq4.safetensors", {"l.sq.codes": ("U8", [4, 128], bytes(512)),
                                            "l.sq.scale": ("F32", [4], _f32(np.ones(4)))}, "4-bit",
              {"tiers": json.dumps({"l": "SQ4"})})
-    _refuses(tmp_path, "sqx.safetensors", t, "without a tier", {"tiers": json.dumps({"l": "SQ3"})})
+    _refuses(tmp_path, "sqx.safetensors", t, "names no SQ tier", {"tiers": json.dumps({"l": "SQ3"})})
 
 
 def test_every_refusal_names_its_rule(tmp_path):
@@ -200,7 +200,7 @@ def test_every_refusal_names_its_rule(tmp_path):
     cq = lambda js: {**t, "w.comfy_quant": _text(js)}                                   # noqa: E731
     cases = [
         ({**t, "w.weight_scale_2": ("F32", [], _f32(1))}, "4-bit layer"),
-        ({**t, "x.weight": ("U8", [4], bytes(4))}, "U8 (4-bit packed"),
+        ({**t, "x.weight": ("U8", [4], bytes(4))}, "uint8 codes"),
         ({**t, "x.scales": ("F8_E8M0", [4], bytes(4))}, "mxfp8"),
         ({**t, "x.weight": ("F8_E5M2", [4], bytes(4))}, "E5M2"),
         ({"x.weight": f8, "x.weight_scale_inv": ("F32", [1, 1], _f32([1]))}, "128×128"),
@@ -209,11 +209,11 @@ def test_every_refusal_names_its_rule(tmp_path):
         (cq({"format": "int8_blockwise"}), 'format "int8_blockwise"'),
         (cq({"format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 8}), "convrot group 8"),
         ({"w.weight": f8, "w.weight_scale": ("F32", [8, 1], _f32(s)),
-          "w.comfy_quant": _text({"format": "float8_e4m3fn", "convrot": True})}, "rotates only int8_tensorwise"),
-        ({**t, "w.comfy_quant": ("U8", [3], b"{x]")}, "not JSON"),
+          "w.comfy_quant": _text({"format": "float8_e4m3fn", "convrot": True})}, "int8_tensorwise weights alone"),
+        ({**t, "w.comfy_quant": ("U8", [3], b"{x]")}, "does not parse as JSON"),
         (cq({"format": "float8_e4m3fn"}), 'I8 declared as "float8_e4m3fn"'),
-        ({"w.weight": ("I8", [8, 16], q.tobytes())}, "int8 without a scale"),
-        ({"w.weight": f8, "w.comfy_quant": _text({"format": "float8_e4m3fn"})}, "published without"),
+        ({"w.weight": ("I8", [8, 16], q.tobytes())}, "no scale for them"),
+        ({"w.weight": f8, "w.comfy_quant": _text({"format": "float8_e4m3fn"})}, "ships no"),
         ({**t, "w.scale_weight": ("F32", [], _f32(1))}, "two scales"),
         ({"w.weight": ("I8", [8, 16], q.tobytes()), "w.weight_scale": ("I32", [8], bytes(32))}, "a scale of type I32"),
         ({"w.weight": ("I8", [8, 16], q.tobytes()), "w.weight_scale": ("F32", [8, 2], bytes(64))}, "shape [8, 2]"),
@@ -222,11 +222,11 @@ def test_every_refusal_names_its_rule(tmp_path):
           "w.comfy_quant": _text({"format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 4})}, "one scale"),
         ({"w.weight": ("I8", [8, 18], bytes(144)), "w.weight_scale": ("F32", [8, 1], _f32(s)),
           "w.comfy_quant": _text({"format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 4})},
-         "input divides"),
+         "multiple of the group"),
         # Subnormal products: an int8 scale under 2^-126; an fp8 one under 2^-117.
         ({"w.weight": ("I8", [8, 16], q.tobytes()), "w.weight_scale": ("F32", [], _f32(2.0 ** -127))}, "subnormal"),
         ({"w.weight": f8, "w.weight_scale": ("F32", [], _f32(2.0 ** -118))}, "subnormal"),
-        ({"x._weight_qdata": ("I8", [8, 16], q.tobytes())}, "without its description"),
+        ({"x._weight_qdata": ("I8", [8, 16], q.tobytes())}, "description is missing"),
         ({"x.weight_thing": ("F32", [1], _f32(1)), "x._weight_extra": ("F32", [1], _f32(1))}, "torchao component"),
     ]
     for i, (tensors, fragment) in enumerate(cases):
@@ -243,14 +243,14 @@ def test_every_refusal_names_its_rule(tmp_path):
         ({"t.weight": json.dumps({"_type": "Int8Tensor", "_tensor_data_names": ["qdata", "act"],
                                   "_data": {"block_size": [1, 16]}})}, base, "torchao parts"),
         ({"t.weight": _torchao("Int8Tensor", "I8", [1, 8])}, base, "torchao block [1, 8]"),
-        ({"t.weight": _torchao("Int8Tensor", "I8", [1, 16], ["zero_point"])}, base, "declared but absent"),
+        ({"t.weight": _torchao("Int8Tensor", "I8", [1, 16], ["zero_point"])}, base, "no tensor holds it"),
         ({"t.weight": _torchao("Int8Tensor", "I8", [1, 16], ["zero_point"])},
          {**base, "t._weight_zero_point": ("I8", [8, 1], bytes([0, 0, 3, 0, 0, 0, 0, 0]))},
-         "zero point 3 on row 2"),
+         "row 2 has zero point 3"),
         ({"t.weight": _torchao("Float8Tensor", "F8_E4M3", [8, 16], fdt="float8_e5m2")},
          {"t._weight_qdata": f8, "t._weight_scale": ("F32", [], _f32(1))}, "float8_e5m2"),
         ({"t.weight": _torchao("Int8Tensor", "I8", [1, 16])},
-         {"t._weight_qdata": ("I8", [8, 16], q.tobytes())}, "scale missing"),
+         {"t._weight_qdata": ("I8", [8, 16], q.tobytes())}, "scale is absent"),
     ]
     for i, (meta, tensors, fragment) in enumerate(ao):
         _refuses(tmp_path, f"ao{i}.safetensors", tensors, fragment, meta)
@@ -333,5 +333,5 @@ def test_the_published_headers_are_recognized_8bit(tmp_path, slug):
         assert qkv and len(r.groups) + 2 * len(qkv) == 270
     if slug == "qwen21-turbo-convrot":
         # CompactTests.swift:325-327: the Turbo's 31 attention preferences, noted and never a tensor.
-        assert any(n.startswith("31 ComfyUI attention preference(s)") for n in r.notes), r.notes
+        assert any(n.startswith("31 ComfyUI attention setting(s)") for n in r.notes), r.notes
         assert all(n in r.consumed for n in st.entries if "comfy_attention" in n)
