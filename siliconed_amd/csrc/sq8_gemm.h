@@ -52,8 +52,8 @@ hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, i
 // kernel with 64- or 32-row tiles of one 64-column slab and the K steps split over four waves
 // (WD_SKINNY64, WD_SKINNY32).
 enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 4, WD_32 = 5 };
-// The tile for an M × N product (GLU: N = 2h): 256 × 256 while those tiles make at least two rounds on
-// the 256 CUs (launch_wdirect takes 128-row tiles where the 256 kernel cannot serve the product), else
+// The tile for an M × N product (GLU: N = 2h): 256 × 256 while those tiles occupy more than half the 256
+// CUs (launch_wdirect takes 128-row tiles where the 256 kernel cannot serve the product), else
 // the tallest of 128, 64 and 32 rows whose tiles number at least 144 (enough to occupy the 256 CUs), else
 // the skinny kernel.
 int choose_wd_tile(int M, int N, bool glu);

@@ -29,11 +29,11 @@ int choose_wd_tile(int M, int N, bool glu) {
     const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
     const long tn = (slabs + 3) / 4;
     auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * (bm == 256 ? (slabs + 3) / 4 : tn); };
-    // 256 × 256 tiles (one workgroup a CU) from two rounds of them on 256 CUs: C1's up-projection,
-    // 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians); C3's fp8 gate-up
-    // (SiLU-GLU, 1280 tiles) 1353 against 1290 TFLOP/s. One round or less (C4's Wo and W_down, 216
-    // tiles) runs faster in 128-row tiles.
-    if (tiles(256) / 2 >= 256) return WD_256;
+    // 256 × 256 tiles (one workgroup a CU) once they occupy more than half the 256 CUs: C1's
+    // up-projection, 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians); C3's fp8
+    // gate-up (SiLU-GLU, 1280 tiles) 1353 against 1290 TFLOP/s; C1's down-projection, 192 tiles (one
+    // partial round), 1208–1228 against 1105. With fewer, the 128-row tiles spread over more CUs.
+    if (tiles(256) > 128) return WD_256;
     if (tiles(128) >= 144) return WD_128;
     if (tiles(64) >= 144) return WD_64;
     if (tiles(32) >= 144) return WD_32;

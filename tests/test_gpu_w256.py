@@ -177,3 +177,4 @@ def test_w256_residual(gemm, orc, tile_gemm, gated):
     gemm.gated_residual(expect, y, gate)
     torch.cuda.synchronize()
     assert bitwise_equal(outs["256"], expect.cpu().numpy()) == 0
+
