@@ -338,7 +338,9 @@ inline bool slab_epilogue_fits(const GemmArgs &p, int epi, int out) {
 }
 
 // LEAN: the slab epilogue (slab_epilogue_fits holds); else each 32 × 32 block through store_block.
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false>
+// NAS: activation stages and weight register buffers (OCC = 2): A(t + NAS − 1) and W(t + NAS) are issued in
+// step t (the 32-row tiles take four: C2's text stream, 512 × 3072 × 3072, 23.5 against 24.9 µs).
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
 gemm_wd_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -351,7 +353,12 @@ gemm_wd_kernel(const GemmArgs p) {
     static_assert(A_PER_WAVE + 4 < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
     // The epilogue regions lie over the A stages (both idle by then); short tiles need more than the stages.
-    constexpr int LDS_STAGES = NW * REGION > 2 * SA ? NW * REGION : 2 * SA;
+    static_assert(NAS == 2 || OCC == 2, "deeper pipelines on the two-workgroup path");
+    constexpr int LDS_STAGES = NW * REGION > NAS * SA ? NW * REGION : NAS * SA;
+    // Loads a wave may leave in flight at the end of step t, A(t+1) and W(t+1) landed: W(t+2) issued in
+    // step t+2−NAS after A(t+1), then every load of the NAS − 2 steps after that one.
+    constexpr int STEP_WAIT = 4 + (NAS - 2) * (A_PER_WAVE + 4);
+    static_assert(STEP_WAIT < 64, "vmcnt budget");
     // The slab epilogue stages the wave's whole BM × 64 bf16 outputs.
     constexpr int LDS_BYTES = LEAN && NW * BM * 128 > LDS_STAGES ? NW * BM * 128 : LDS_STAGES;
     static_assert(!LEAN || (OUT == OUT_BF16 && (EPI == EPI_NONE || EPI == EPI_GELU)), "slab epilogue: bf16, plain or GELU");
@@ -392,7 +399,7 @@ gemm_wd_kernel(const GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, j, lane);
     const uint32_t w_step = WL == W_PACKED ? 4096 : BK;
-    u32x4 raw[2][4];
+    u32x4 raw[NAS][4];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
         const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
@@ -469,19 +476,31 @@ gemm_wd_kernel(const GemmArgs p) {
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
 
-    // Prologue: A(0) → stage 0, W(0) → raw[0], W(1) → raw[1]; A(0) and W(0) landed.
-    issue_a(0, I0{});
-    issue_w(0, I0{});
-    issue_w(1, I1{});
-    wait_vmcnt<4>();
-    if constexpr (OCC == 1) widen_all(I0{}, I0{});
+    if constexpr (NAS == 2) {
+        // Prologue: A(0) → stage 0, W(0) → raw[0], W(1) → raw[1]; A(0) and W(0) landed.
+        issue_a(0, I0{});
+        issue_w(0, I0{});
+        issue_w(1, I1{});
+        wait_vmcnt<4>();
+        if constexpr (OCC == 1) widen_all(I0{}, I0{});
+    } else {
+        // Prologue in the steps' issue order: A(0 .. NAS−2) and W(0 .. NAS−1), all landed.
+        static_for<0, NAS>([&](auto vc) {
+            constexpr int v = decltype(vc)::value;
+            if constexpr (v > 0) issue_a(v - 1, std::integral_constant<int, v - 1>{});
+            issue_w(v, vc);
+        });
+        wait_vmcnt<0>();
+    }
     step_barrier();
 
     // OCC = 2: the codes of W(t) are widened just in time, one sub-step ahead of the MFMAs that use
     // them, like the activation fragments: two sub-steps of fragments are live at a time (the
     // registers a full step of widened codes would take are what lets the fragment reads be
     // double-buffered). raw[P] is free once sub-step 3 is widened: W(t+2) is issued then.
-    auto step_jit = [&](int t, auto par) {
+    // Step t reads activation stage S and widens raw[P] (NAS = 2: S = P = t mod 2).
+    auto step_jit = [&](int t, auto stc, auto par) {
+        constexpr int S = decltype(stc)::value;
         constexpr int P = decltype(par)::value;
         bf16x8 wk[2][2];  // [ks & 1][block]
         bf16x8 xf[2][FM];
@@ -497,13 +516,14 @@ gemm_wd_kernel(const GemmArgs p) {
             constexpr int ks = decltype(kc)::value;
             static_for<0, FM>([&](auto bmc) {
                 constexpr int bm = decltype(bmc)::value;
-                xf[ks & 1][bm] = kern::lds_load_frag(lds + P * SA + 32 * 128 * bm, xo[bm & 1][ks]);
+                xf[ks & 1][bm] = kern::lds_load_frag(lds + S * SA + 32 * 128 * bm, xo[bm & 1][ks]);
             });
         };
         __builtin_amdgcn_sched_barrier(0);
         read_x(I0{});
         widen_ks(I0{});
-        issue_a(t + 1, std::integral_constant<int, 1 - P>{});
+        // Into the stage read in step t − 1 (the barrier that ended it saw every wave's reads).
+        issue_a(t + NAS - 1, std::integral_constant<int, (S + NAS - 1) % NAS>{});
         static_for<0, 4>([&](auto kc) {
             constexpr int ks = decltype(kc)::value;
             if constexpr (ks < 3) {
@@ -513,7 +533,7 @@ gemm_wd_kernel(const GemmArgs p) {
             if constexpr (ks == 2) {
                 // The A loads stay ahead of these in issue order (the vmcnt counts rely on it).
                 __builtin_amdgcn_sched_barrier(0);
-                issue_w(t + 2, std::integral_constant<int, P>{});
+                issue_w(t + NAS, std::integral_constant<int, P>{});
                 __builtin_amdgcn_sched_barrier(0);
             }
             static_for<0, 2>([&](auto bc) {
@@ -534,7 +554,7 @@ gemm_wd_kernel(const GemmArgs p) {
             __builtin_amdgcn_sched_barrier(0);
         });
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<4>();
+        wait_vmcnt<STEP_WAIT>();
         step_barrier();
     };
 
@@ -543,7 +563,7 @@ gemm_wd_kernel(const GemmArgs p) {
     auto one_step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         if constexpr (OCC == 2) {
-            step_jit(t, par);
+            step_jit(t, par, par);
         } else {
             issue_a(t + 1, std::integral_constant<int, 1 - P>{});
             issue_w(t + 2, std::integral_constant<int, P>{});
@@ -556,12 +576,22 @@ gemm_wd_kernel(const GemmArgs p) {
             step_barrier();
         }
     };
-    int t = 0;
-    for (; t + 1 < KT; t += 2) {
-        one_step(t, I0{});
-        one_step(t + 1, I1{});
+    if constexpr (NAS == 2) {
+        int t = 0;
+        for (; t + 1 < KT; t += 2) {
+            one_step(t, I0{});
+            one_step(t + 1, I1{});
+        }
+        if (t < KT) one_step(t, I0{});
+    } else {
+        // Step t + u on stage and buffer u.
+        int t = 0;
+        for (; t + NAS <= KT; t += NAS)
+            static_for<0, NAS>([&](auto uc) { step_jit(t + decltype(uc)::value, uc, uc); });
+        static_for<0, NAS - 1>([&](auto uc) {
+            if (t + decltype(uc)::value < KT) step_jit(t + decltype(uc)::value, uc, uc);
+        });
     }
-    if (t < KT) one_step(t, I0{});
     // The scales and biases of the wave's columns, loaded once for all its row blocks; their latency
     // overlaps the wait below.
     const bool has_bias = p.bias != nullptr;
@@ -601,7 +631,7 @@ gemm_wd_kernel(const GemmArgs p) {
     });
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false>
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2>
 hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
@@ -610,17 +640,17 @@ hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = (slabs + NW - 1) / NW;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN, NAS>), dim3(blocks), dim3(64 * NW), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int OCC, int WT, int WL>
+template <int BM, int NW, int OCC, int WT, int WL, int NAS = 2>
 hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) {
     if (slab_epilogue_fits(p, epi, out))
-        return epi == EPI_GELU ? launch_wd<BM, NW, OCC, WT, WL, EPI_GELU, OUT_BF16, true>(p, stream)
-                               : launch_wd<BM, NW, OCC, WT, WL, EPI_NONE, OUT_BF16, true>(p, stream);
+        return epi == EPI_GELU ? launch_wd<BM, NW, OCC, WT, WL, EPI_GELU, OUT_BF16, true, NAS>(p, stream)
+                               : launch_wd<BM, NW, OCC, WT, WL, EPI_NONE, OUT_BF16, true, NAS>(p, stream);
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O>(p, stream);
+    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O, false, NAS>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
