@@ -1,13 +1,14 @@
 """A map's 8-bit weights staged for the product (siliconed_amd.artifact.Artifact.stage): the same
 bits as the product on the same codes passed directly — int8 with a convrot rotation, fp8 with a bf16
-scale per column, int8 with one scale for the tensor."""
+scale per column, int8 with one scale for the tensor — and each judged against the oracle's fp64 truth of
+its codes (the convrot one on x·R rounded to bf16, as the reference rounds the rotated operand)."""
 import numpy as np
 import pytest
 import torch
 
 from refgen import bitwise_equal
 from siliconed_amd.artifact import Artifact, MapTensor, write_map
-from test_gpu_parity import bf16_dev, dev
+from test_gpu_parity import bf16_dev, dev, judge
 
 pytestmark = pytest.mark.gpu
 
@@ -38,3 +39,9 @@ def test_staged_weights_give_the_products_of_their_codes(gemm, orc, tmp_path):
     torch.cuda.synchronize()
     for got, want in ((got_a, want_a), (got_b, want_b), (got_c, want_c)):
         assert bitwise_equal(got.cpu().numpy(), want.cpu().numpy()) == 0
+    qt = np.ascontiguousarray(q.T).view(np.uint8)
+    ft = np.ascontiguousarray(f8.T).view(np.uint8)
+    xr = orc.f32_to_bf16(orc.rotate_groups(orc.bf16_to_f32(x), 256))
+    judge(orc, got_a.cpu().numpy(), xr, qt, False, s, None, "none", torch.float32)
+    judge(orc, got_b.cpu().numpy(), x, ft, True, orc.bf16_to_f32(sb), None, "none", torch.float32)
+    judge(orc, got_c.cpu().numpy(), x, qt, False, np.full(n, 0.0123, np.float32), None, "none", torch.float32)
