@@ -28,12 +28,19 @@ int choose_wd_tile(int M, int N, bool glu) {
     // 64-row above (M = 16: 8.3 µs against 20.2 for 32-row tiles of the main kernel).
     const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
     const long tn = (slabs + 3) / 4;
-    auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * (bm == 256 ? (slabs + 3) / 4 : tn); };
+    auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * tn; };
     // 256 × 256 tiles (one workgroup a CU) once they occupy more than half the 256 CUs: C1's
     // up-projection, 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians); C3's fp8
     // gate-up (SiLU-GLU, 1280 tiles) 1353 against 1290 TFLOP/s; C1's down-projection, 192 tiles (one
     // partial round), 1208–1228 against 1105. With fewer, the 128-row tiles spread over more CUs.
-    if (tiles(256) > 128) return WD_256;
+    if (tiles(256) > 128) {
+        // 224-row tiles where their rounds on the 256 CUs cover fewer rows than the 256-row tiles' (the
+        // same work per row, one workgroup a CU): C1's down-projection (M = 4096, N = 3072) 228 tiles in
+        // one round against 192 in one; C4's and C2's fused QKV (M = 4608, N = 9216) 756 tiles in three
+        // rounds against 648 in three; never C1's up-projection (768 tiles, three full rounds).
+        auto rows = [&](int bm) { return (tiles(bm) + 255) / 256 * bm; };
+        return rows(224) < rows(256) ? WD_224 : WD_256;
+    }
     if (tiles(128) >= 144) return WD_128;
     if (tiles(64) >= 144) return WD_64;
     if (tiles(32) >= 144) return WD_32;

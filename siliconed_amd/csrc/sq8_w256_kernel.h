@@ -1,5 +1,7 @@
 // sq8_w256_kernel.h — the weight-direct GEMM in 256 × 256 tiles, one workgroup of four waves per CU:
-// the large-product kernel (C1's up-projection: 768 tiles, three rounds on 256 CUs).
+// the large-product kernel (C1's up-projection: 768 tiles, three rounds on 256 CUs). The same kernel in
+// 224 × 256 tiles (BM = 224: 7 row blocks a wave) serves products whose 256-row tiles would leave the last
+// round partly empty (C1's down-projection: 228 tiles in one round against 192).
 //
 // Arithmetic as the other kernels (Sources/Siliconed/TensorGEMM.swift:124-135, :173-179):
 // C = act(s ⊙ (A·q) + b), exact bf16 × code products, fp32 sums, scale after the sum, bias after the
@@ -36,15 +38,16 @@
 namespace sq8 {
 namespace wd {
 
-template <int WT, int WL, int EPI, int OUT>
+template <int WT, int WL, int EPI, int OUT, int BM = 256>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 gemm_w256_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr bool SLAB = (EPI == EPI_NONE || EPI == EPI_GELU) && OUT == OUT_BF16;
     static_assert(EPI != EPI_RESIDUAL || OUT == OUT_F32, "the residual stream is fp32");
-    constexpr int BM = 256, NW = 4, FM = 8, NAS = 4;
+    static_assert(BM == 256 || BM == 224, "256- or 224-row tiles");
+    constexpr int NW = 4, FM = BM / 32, NAS = 4;
     constexpr int SA = BM * 128;             // bytes per activation stage
-    constexpr int A_PER_WAVE = BM / 8 / NW;  // 1 KB direct loads per wave per step
+    constexpr int A_PER_WAVE = BM / 8 / NW;  // 1 KB direct loads per wave per step (8 or 7)
     constexpr int SB_OFF = NAS * SA;         // the tile's scales (1 KB) then biases (1 KB)
     constexpr int LDS_BYTES = SB_OFF + 2048;
     static_assert(NW * BM * 128 <= SB_OFF, "the epilogue regions lie over the stages");
@@ -93,13 +96,14 @@ gemm_w256_kernel(const GemmArgs p) {
             __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024),
                                              16, 0, 0);
     };
-    auto issue_a2 = [&](int t, auto stage, auto part) {  // rows blocks 2·part, 2·part + 1
+    auto issue_a2 = [&](int t, auto stage, auto part) {  // rows blocks 2·part, 2·part + 1 (those there are)
         constexpr int S = decltype(stage)::value, Q = decltype(part)::value;
         const kern::gbytes base = Ag + (uint32_t)min(t, KT - 1) * (BK * 2);
         static_for<2 * Q, 2 * Q + 2>([&](auto ic) {
             constexpr int i = decltype(ic)::value;
-            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024),
-                                             16, 0, 0);
+            if constexpr (i < A_PER_WAVE)
+                __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]),
+                                                 (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024), 16, 0, 0);
         });
     };
 
@@ -162,15 +166,19 @@ gemm_w256_kernel(const GemmArgs p) {
             });
         });
     };
-    // One sub-step's schedule: 16 MFMAs, between them the next fragments' 8 LDS reads, the next codes'
-    // 24 widening operations and 3 global loads.
-    auto interleave = [&]() {
-        static_for<0, 16>([&](auto ic) {
+    // Sub-step Q's schedule: 2·FM MFMAs, between them the next fragments' FM LDS reads, the next codes'
+    // 24 widening operations and the sub-step's global loads (two activation rows blocks, those there
+    // are, and one weight load).
+    auto interleave = [&](auto part) {
+        constexpr int Q = decltype(part)::value;
+        constexpr int VMEM = (2 * Q < A_PER_WAVE) + (2 * Q + 1 < A_PER_WAVE) + 1;
+        static_for<0, 2 * FM>([&](auto ic) {
             constexpr int i = decltype(ic)::value;
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if constexpr (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if constexpr (i < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             if constexpr (i < 12) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-            if constexpr (i == 1 || i == 5 || i == 9) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            if constexpr ((i == 1 && VMEM > 0) || (i == 5 && VMEM > 1) || (i == 9 && VMEM > 2))
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         });
     };
     using I0 = std::integral_constant<int, 0>;
@@ -212,7 +220,7 @@ gemm_w256_kernel(const GemmArgs p) {
             issue_a2(s + 3, S3{}, kc);
             issue_w1(s + 3, S3{}, kc);
             mfma_ks(std::integral_constant<int, ks & 1>{});
-            interleave();
+            interleave(kc);
             __builtin_amdgcn_sched_barrier(0);
         });
         wait_vmcnt<A_PER_WAVE + 4>();
@@ -289,17 +297,17 @@ inline bool w256_fits(const GemmArgs &p, int epi, int out) {
     return true;
 }
 
-template <int WT, int WL>
+template <int WT, int WL, int BM = 256>
 hipError_t launch_w256(const GemmArgs &args, int epi, int out, hipStream_t stream) {
     GemmArgs p = args;
     const bool glu = epi == EPI_SILU_GLU || epi == EPI_SITU_GLU;
-    p.tiles_m = (p.M + 255) / 256;
+    p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = glu ? (p.glu_half / 32 + 3) / 4 : (p.N + 255) / 256;
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
 #define SQ8_CASE(E, O)                                                                                   \
     if (epi == E && out == O) {                                                                          \
-        hipLaunchKernelGGL((gemm_w256_kernel<WT, WL, E, O>), dim3(blocks), dim3(256), 0, stream, p);  \
+        hipLaunchKernelGGL((gemm_w256_kernel<WT, WL, E, O, BM>), dim3(blocks), dim3(256), 0, stream, p); \
         return hipGetLastError();                                                                        \
     }
     SQ8_CASE(EPI_NONE, OUT_BF16)

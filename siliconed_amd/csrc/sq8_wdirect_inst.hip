@@ -14,10 +14,12 @@ namespace sq8 {
 
 hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const GemmArgs &p, int tile, int epi, int out,
                                                                        hipStream_t stream) {
-    // 256 × 256 tiles where their kernel serves the product (whole slabs, aligned scales and biases);
-    // else the two-workgroup 128-row tiles.
-    if (tile == WD_256) {
-        if (wd::w256_fits(p, epi, out)) return wd::launch_w256<SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    // 256 × 256 or 224 × 256 tiles where their kernel serves the product (whole slabs, aligned scales and
+    // biases); else the two-workgroup 128-row tiles.
+    if (tile == WD_256 || tile == WD_224) {
+        if (wd::w256_fits(p, epi, out))
+            return tile == WD_256 ? wd::launch_w256<SQ8_WT, SQ8_WL, 256>(p, epi, out, stream)
+                                  : wd::launch_w256<SQ8_WT, SQ8_WL, 224>(p, epi, out, stream);
         tile = WD_128;
     }
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);

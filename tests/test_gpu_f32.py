@@ -73,7 +73,7 @@ def test_rounded_route_misses_the_fp32_bar(gemm, orc):
     assert judge(orc, e.cpu().numpy(), x, q, False, s, b, "none", torch.float32) <= 1e-6
 
 
-KERNEL_KNOBS = {"main256": "256", "main128": "128", "main64": "64", "main32": "32", "skinny64": "s64",
+KERNEL_KNOBS = {"main256": "256", "main224": "224", "main128": "128", "main64": "64", "main32": "32", "skinny64": "s64",
                 "skinny32": "s32"}
 
 

@@ -353,7 +353,7 @@ def test_packed_baseline_shapes(gemm, orc, case):
 
 # ---- every weight-direct kernel on the same problems ----------------------------------------------
 
-TILES = {"main128": "128", "main256": "256", "skinny64": "s64", "skinny32": "s32"}
+TILES = {"main128": "128", "main256": "256", "main224": "224", "skinny64": "s64", "skinny32": "s32"}
 KERNEL_SHAPES = [
     (1, 64, 64),       # one K step: three of the skinny kernel's four waves have none
     (33, 320, 200),    # 5 K steps (not a multiple of the 4 waves), ragged M and N
@@ -379,6 +379,9 @@ def test_each_kernel_on_the_same_problem(gemm, orc, tile_gemm, shape, fp8):
     # Same kernel, same K order: the skinny kernel gives the same bits whatever its tile height.
     for out in (torch.float32, torch.bfloat16):
         assert torch.equal(results[("skinny64", out)], results[("skinny32", out)])
+        # The main kernels: one MFMA sequence over K at every height.
+        assert torch.equal(results[("main256", out)], results[("main128", out)])
+        assert torch.equal(results[("main224", out)], results[("main128", out)])
 
 
 @pytest.mark.parametrize("epi", ["silu", "situ"])

@@ -1,8 +1,9 @@
-"""The 256 × 256 kernel (one workgroup per CU), its slab and block epilogues, on an MI355X.
+"""The 256 × 256 kernel (one workgroup per CU) in 256- and 224-row tiles, its slab and block epilogues, on
+an MI355X.
 
 Every output of the weight-direct kernels is one MFMA sequence over K whatever the tile, and the slab
-epilogue applies the same scale, bias and activation as the 32 × 32-block one: so the 256-row tiles
-give the same bits as the 128-row tiles, and both are judged against the oracle's fp64 truth on
+epilogue applies the same scale, bias and activation as the 32 × 32-block one: so the 256- and 224-row
+tiles give the same bits as the 128-row tiles, and they are judged against the oracle's fp64 truth on
 sampled rows at the reference's bars (DiagnosticProbes.swift:75-82, DiagnosticJudgement.swift:39-71).
 Shapes cover a ragged last row tile, a last column tile with fewer slabs than waves, per-tensor scales,
 no bias, fp8 codes, both weight layouts, the QKV split (row-major and head-major), the GLU epilogues,
@@ -40,8 +41,10 @@ def test_w256_same_bits_as_128(gemm, orc, tile_gemm, m, k, n, fp8, layout, epi, 
     if layout == "packed":
         w = gemm.pack(w, layout="nk")
     y256 = product(tile_gemm, "256", x, w, s, b, "nk", epi)
+    y224 = product(tile_gemm, "224", x, w, s, b, "nk", epi)
     y128 = product(tile_gemm, "128", x, w, s, b, "nk", epi)
     assert bitwise_equal(y256, y128) == 0
+    assert bitwise_equal(y224, y128) == 0
     sj = np.full(n, s[0], dtype=np.float32) if tensor_scale else s
     judge(orc, y256, x, q, fp8, sj, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
 
@@ -53,8 +56,10 @@ def test_w256_fp32_output(gemm, orc, tile_gemm):
     x, q, s, b = problem(orc, m, k, n, False, 91)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     y256 = product(tile_gemm, "256", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
+    y224 = product(tile_gemm, "224", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
     y128 = product(tile_gemm, "128", x, w, s, b, "nk", "gelu", out_dtype=torch.float32)
     assert bitwise_equal(y256, y128) == 0
+    assert bitwise_equal(y224, y128) == 0
     judge(orc, y256, x, q, False, s, b, "gelu", torch.float32, rows=orc.sample_rows(m, 64))
 
 
@@ -66,7 +71,7 @@ def test_w256_qkv(gemm, orc, tile_gemm, head_dim):
     x, q, s, b = problem(orc, m, k, 3 * d, False, 77 + head_dim)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     outs = {}
-    for tile in ("256", "128"):
+    for tile in ("256", "224", "128"):
         qq, kk, vv = tile_gemm(tile).product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
         torch.cuda.synchronize()
         parts = []
@@ -77,6 +82,7 @@ def test_w256_qkv(gemm, orc, tile_gemm, head_dim):
             parts.append(t.cpu().numpy())
         outs[tile] = np.concatenate(parts, axis=1)
     assert bitwise_equal(outs["256"], outs["128"]) == 0
+    assert bitwise_equal(outs["224"], outs["128"]) == 0
     judge(orc, outs["256"], x, q, False, s, b, "none", torch.bfloat16, rows=orc.sample_rows(m, 64))
 
 
@@ -127,11 +133,12 @@ def test_w256_on_the_fp32_route(gemm, orc, tile_gemm):
     b = orc.normal_f32(84, (n,), 0.0, 0.02)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     outs = {}
-    for tile in ("256", "128"):
+    for tile in ("256", "224", "128"):
         y = tile_gemm(tile).product(dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh", rounding=False)
         torch.cuda.synchronize()
         outs[tile] = y.float().cpu().numpy()
     assert bitwise_equal(outs["256"], outs["128"]) == 0
+    assert bitwise_equal(outs["224"], outs["128"]) == 0
     judge(orc, outs["256"], x, q, False, s, b, "gelu", torch.bfloat16, rows=orc.sample_rows(m, 64))
 
 
@@ -148,11 +155,12 @@ def test_w256_glu(gemm, orc, tile_gemm, epi, h, fp8, layout):
     name = {"silu": "silu_glu", "situ": "situ_glu"}[epi]
     for out in (torch.bfloat16, torch.float32):
         ys = {}
-        for tile in ("256", "128"):
+        for tile in ("256", "224", "128"):
             y = tile_gemm(tile).product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), epilogue=name, out_dtype=out)
             torch.cuda.synchronize()
             ys[tile] = y.float().cpu().numpy()
         assert bitwise_equal(ys["256"], ys["128"]) == 0
+        assert bitwise_equal(ys["224"], ys["128"]) == 0
         judge(orc, ys["256"], x, q, fp8, s, b, epi, out, rows=orc.sample_rows(m, 64))
 
 
@@ -166,12 +174,13 @@ def test_w256_residual(gemm, orc, tile_gemm, gated):
     gate = dev(orc.normal_f32(84, (n,), 0.0, 0.5)) if gated else None
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     outs = {}
-    for tile in ("256", "128"):
+    for tile in ("256", "224", "128"):
         got = dev(stream)
         tile_gemm(tile).product_residual(got, bf16_dev(x_), w, dev(s), bias=dev(b), gate=gate)
         torch.cuda.synchronize()
         outs[tile] = got.cpu().numpy()
     assert bitwise_equal(outs["256"], outs["128"]) == 0
+    assert bitwise_equal(outs["224"], outs["128"]) == 0
     y = tile_gemm("256").product(bf16_dev(x_), w, dev(s), bias=dev(b), out_dtype=torch.float32)
     expect = dev(stream)
     gemm.gated_residual(expect, y, gate)
