@@ -42,7 +42,7 @@ RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # hbm_traffic_and_mfma_busy_by_workload.md).
 TRAFFIC_BYTES = {("c1_up", "packed"): 403.6e6, ("c2_skinny", "packed"): 47.47e6, ("c0", "packed"): 56.95e6,
                  ("skinny_m1", "packed"): 9.70e6, ("skinny_m16", "packed"): 10.53e6, ("skinny_m64", "packed"): 13.19e6,
-                 ("c1_down", "packed"): 378.0e6, ("c2_qkv", "packed"): 403.5e6, ("c3_gate_up", "packed"): 716.4e6,
+                 ("c1_down", "packed"): 450.3e6, ("c2_qkv", "packed"): 415.5e6, ("c3_gate_up", "packed"): 716.4e6,
                  ("c3_down", "packed"): 367.5e6, ("c3_plain", "packed"): 479.0e6, ("c1_w8a8", "packed"): 472.3e6,
                  ("c1_q8", "packed"): 592.2e6, ("c1_f32", "packed"): 1007.6e6, ("c1_convrot", "packed"): 403.7e6}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
