@@ -105,12 +105,14 @@ __device__ __forceinline__ float tanh_fast(float y) {
 
 // GELU-tanh: ½·x·(1 + tanh(u)) with u = √(2/π)·(x + 0.044715·x³), computed as its identical form
 // x·σ(2u) = x / (1 + e^{−2u}) — one exponential and one reciprocal; e^{−2u} overflowing gives
-// x/∞ = −0 for large negative x, as the tanh form's ½·x·0.
+// x/∞ = −0 for large negative x, as the tanh form's ½·x·0. The exponent −2u·log2(e) is
+// x·(k + k·0.044715·x²), k = −2·√(2/π)·log2(e), its constant folded into the polynomial (seven
+// vector instructions a value).
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float k = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // −2·√(2/π)·log2(e)
-    const float x2 = x * x;
-    const float q = x * __builtin_fmaf(0.044715f, x2, 1.0f);
-    const float e = __builtin_amdgcn_exp2f(q * k);
+    constexpr float k = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634);
+    constexpr float k3 = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634 * 0.044715);
+    const float t = __builtin_fmaf(k3, x * x, k);
+    const float e = __builtin_amdgcn_exp2f(x * t);
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

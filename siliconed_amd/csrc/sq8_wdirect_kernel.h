@@ -239,9 +239,8 @@ __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_
 // Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
 // `x` (and `u`, with `cu`), written to the wave's LDS region as rows of 32 values, then stored as
 // 16-byte row segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
-template <int EPI, int OUT>
-__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
-                                            const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
+template <int EPI, int OUT, bool HB>
+__device__ __forceinline__ void stage_block(const f32x16 &x, const ColParams &cx, const f32x16 &u, const ColParams &cu,
                                             uint8_t *region, int lane) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
@@ -254,12 +253,12 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
         static_for<0, 4>([&](auto ec) {
             constexpr int e = decltype(ec)::value;
             float v = __fmul_rn(x[4 * g + e], cx.s[g][e]);
-            if (has_bias) v = __fadd_rn(v, cx.b[g][e]);
+            if constexpr (HB) v = __fadd_rn(v, cx.b[g][e]);
             if constexpr (EPI == EPI_GELU) {
                 v = gelu_tanh(v);
             } else if constexpr (GLU) {
                 float w = __fmul_rn(u[4 * g + e], cu.s[g][e]);
-                if (has_bias) w = __fadd_rn(w, cu.b[g][e]);
+                if constexpr (HB) w = __fadd_rn(w, cu.b[g][e]);
                 v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
             }
             y[e] = v;
@@ -270,6 +269,17 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
         else
             *reinterpret_cast<f32x4 *>(dst) = f32x4{y[0], y[1], y[2], y[3]};
     });
+}
+
+// (The bias test is one uniform branch around the whole block, not a select per value.)
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
+                                            const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
+                                            uint8_t *region, int lane) {
+    if (has_bias)
+        stage_block<EPI, OUT, true>(x, cx, u, cu, region, lane);
+    else
+        stage_block<EPI, OUT, false>(x, cx, u, cu, region, lane);
     flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
 }
 
@@ -279,9 +289,9 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
 // back as 16-byte chunks, eight lanes a row, so each store instruction writes eight whole 128-byte
 // row segments. No wait between the blocks: all values are staged, then all are stored. Rows past M
 // are not stored. `region`: 32·FM·128 bytes of the wave's own.
-template <int FM, int EPI>
-__device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x16 (&acc)[2][FM], const ColParams (&cp)[2],
-                                                   bool has_bias, int m0, int col0, uint8_t *region, int lane) {
+template <int FM, int EPI, bool HB>
+__device__ __forceinline__ void stage_slab_bf16(const f32x16 (&acc)[2][FM], const ColParams (&cp)[2], uint8_t *region,
+                                                int lane) {
     const int h = lane >> 5, r = lane & 31;
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
@@ -293,7 +303,7 @@ __device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x
                 static_for<0, 4>([&](auto ec) {
                     constexpr int e = decltype(ec)::value;
                     float v = __fmul_rn(acc[b][bm][4 * g + e], cp[b].s[g][e]);
-                    if (has_bias) v = __fadd_rn(v, cp[b].b[g][e]);
+                    if constexpr (HB) v = __fadd_rn(v, cp[b].b[g][e]);
                     if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
                     y[e] = v;
                 });
@@ -304,6 +314,16 @@ __device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x
             });
         });
     });
+}
+
+// (The bias test is one uniform branch around the whole slab, not a select per value.)
+template <int FM, int EPI>
+__device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x16 (&acc)[2][FM], const ColParams (&cp)[2],
+                                                   bool has_bias, int m0, int col0, uint8_t *region, int lane) {
+    if (has_bias)
+        stage_slab_bf16<FM, EPI, true>(acc, cp, region, lane);
+    else
+        stage_slab_bf16<FM, EPI, false>(acc, cp, region, lane);
     // Where the slab's rows go: output `which` of the QKV split, then row-major (ldc) or head-major
     // ([heads, M, head_dim]: consecutive rows of one head are head_dim apart).
     int which = 0, cc = col0;
