@@ -24,6 +24,11 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
     }
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_64) return wd::dispatch_wd<64, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile == WD_64N) {
+        // One 32-column block a wave: not for the GLU epilogues (a wave needs both halves' blocks).
+        if (p.glu_half == 0) return wd::dispatch_wd<64, 4, 2, SQ8_WT, SQ8_WL, 2, 1>(p, epi, out, stream);
+        tile = WD_32;
+    }
     if (tile == WD_32) return wd::dispatch_wd<32, 4, 2, SQ8_WT, SQ8_WL, 4>(p, epi, out, stream);
     if (tile == WD_SKINNY64) return wd::dispatch_skinny<64, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_SKINNY32) return wd::dispatch_skinny<32, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);

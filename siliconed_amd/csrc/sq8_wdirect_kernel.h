@@ -360,7 +360,10 @@ inline bool slab_epilogue_fits(const GemmArgs &p, int epi, int out) {
 // LEAN: the slab epilogue (slab_epilogue_fits holds); else each 32 × 32 block through store_block.
 // NAS: activation stages and weight register buffers (OCC = 2): A(t + NAS − 1) and W(t + NAS) are issued in
 // step t (the 32-row tiles take four: C2's text stream, 512 × 3072 × 3072, 23.5 against 24.9 µs).
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2>
+// CB: 32-column blocks a wave owns — 2 (a 64-column slab, tiles BM × 64·NW) or 1 (wave w: block w & 1 of
+// slab w ÷ 2, tiles BM × 32·NW; no GLU, no slab epilogue, two workgroups a CU): half the codes a wave widens
+// per MFMA.
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2>
 __global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
 gemm_wd_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
@@ -368,16 +371,18 @@ gemm_wd_kernel(const GemmArgs p) {
     constexpr int SA = BM * 128;                     // bytes per A stage
     constexpr int A_BLOCKS = BM / 8;                 // 1 KB (8-row) blocks per A stage
     constexpr int A_PER_WAVE = A_BLOCKS / NW;
+    constexpr int WLD = 2 * CB;                      // 16-byte weight loads per lane per K step
+    static_assert(CB == 2 || (CB == 1 && !GLU && !LEAN && OCC == 2), "one-block waves: no GLU, block epilogue");
     // Every wave issues the same number of activation loads, so one vmcnt value fits them all.
     static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
-    static_assert(A_PER_WAVE + 4 < 64, "vmcnt budget");
+    static_assert(A_PER_WAVE + WLD < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
     // The epilogue regions lie over the A stages (both idle by then); short tiles need more than the stages.
     static_assert(NAS == 2 || OCC == 2, "deeper pipelines on the two-workgroup path");
     constexpr int LDS_STAGES = NW * REGION > NAS * SA ? NW * REGION : NAS * SA;
     // Loads a wave may leave in flight at the end of step t, A(t+1) and W(t+1) landed: W(t+2) issued in
     // step t+2−NAS after A(t+1), then every load of the NAS − 2 steps after that one.
-    constexpr int STEP_WAIT = 4 + (NAS - 2) * (A_PER_WAVE + 4);
+    constexpr int STEP_WAIT = WLD + (NAS - 2) * (A_PER_WAVE + WLD);
     static_assert(STEP_WAIT < 64, "vmcnt budget");
     // The slab epilogue stages the wave's whole BM × 64 bf16 outputs.
     constexpr int LDS_BYTES = LEAN && NW * BM * 128 > LDS_STAGES ? NW * BM * 128 : LDS_STAGES;
@@ -390,7 +395,9 @@ gemm_wd_kernel(const GemmArgs p) {
     int tm, tn;
     kern::tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM;
-    const int slab = tn * NW + wave;
+    // The wave's weight columns: slab `slab`, blocks [b0, b0 + CB).
+    const int slab = CB == 2 ? tn * NW + wave : tn * (NW / 2) + (wave >> 1);
+    const int b0 = CB == 2 ? 0 : (wave & 1);
     const kern::gbytes Ag = (kern::gbytes)p.a;
     const kern::gbytes Wg = (kern::gbytes)p.w;
     const int KT = p.kt;
@@ -414,24 +421,24 @@ gemm_wd_kernel(const GemmArgs p) {
                                              16, 0, 0);
     };
 
-    // ---- weight loads: 4 × 16 bytes per lane per K step --------------------------------------------
-    uint32_t w_off[4];
+    // ---- weight loads: WLD × 16 bytes per lane per K step (load j: block b0 + j ÷ 2, half j & 1) ------
+    uint32_t w_off[WLD];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, j, lane);
+    for (int j = 0; j < WLD; ++j) w_off[j] = w_offset<WL, GLU>(p, slab, 2 * b0 + j, lane);
     const uint32_t w_step = WL == W_PACKED ? 4096 : BK;
-    u32x4 raw[NAS][4];
+    u32x4 raw[NAS][WLD];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
         const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
+        for (int j = 0; j < WLD; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
     };
 
     // ---- fragments -----------------------------------------------------------------------------------
-    bf16x8 wf[2][2][4];  // OCC = 1: [buffer][block][ks]
+    bf16x8 wf[2][CB][4];  // OCC = 1: [buffer][block][ks]
     auto widen_all = [&](auto src, auto dst) {
         constexpr int S = decltype(src)::value, D = decltype(dst)::value;
-        static_for<0, 2>([&](auto bc) {
+        static_for<0, CB>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
             static_for<0, 4>([&](auto kc) {
                 constexpr int ks = decltype(kc)::value;
@@ -450,9 +457,9 @@ gemm_wd_kernel(const GemmArgs p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) xo[par][ks] = swz(32 * par + (lane & 31), 4 * h + ks) - 32 * 128 * par;
 
-    f32x16 acc[2][FM];
+    f32x16 acc[CB][FM];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < CB; ++b)
 #pragma unroll
         for (int bm = 0; bm < FM; ++bm)
 #pragma unroll
@@ -474,7 +481,7 @@ gemm_wd_kernel(const GemmArgs p) {
         static_for<0, 4>([&](auto kc) {
             constexpr int ks = decltype(kc)::value;
             if constexpr (ks < 3) read_x(std::integral_constant<int, ks + 1>{}, std::integral_constant<int, (ks + 1) & 1>{});
-            if constexpr (OCC == 1) {
+            if constexpr (OCC == 1 && CB == 2) {
                 // Widen the next step's block ks >> 1, sub-steps 2(ks & 1) and 2(ks & 1) + 1.
                 constexpr int b = ks >> 1;
                 static_for<0, 2>([&](auto qc) {
@@ -483,7 +490,7 @@ gemm_wd_kernel(const GemmArgs p) {
                     wf[1 - F][b][q] = widen8<WT>(r[2 * (q & 1)], r[2 * (q & 1) + 1]);
                 });
             }
-            static_for<0, 2>([&](auto bc) {
+            static_for<0, CB>([&](auto bc) {
                 constexpr int b = decltype(bc)::value;
                 static_for<0, FM>([&](auto bmc) {
                     constexpr int bm = decltype(bmc)::value;
@@ -501,7 +508,7 @@ gemm_wd_kernel(const GemmArgs p) {
         issue_a(0, I0{});
         issue_w(0, I0{});
         issue_w(1, I1{});
-        wait_vmcnt<4>();
+        wait_vmcnt<WLD>();
         if constexpr (OCC == 1) widen_all(I0{}, I0{});
     } else {
         // Prologue in the steps' issue order: A(0 .. NAS−2) and W(0 .. NAS−1), all landed.
@@ -522,11 +529,11 @@ gemm_wd_kernel(const GemmArgs p) {
     auto step_jit = [&](int t, auto stc, auto par) {
         constexpr int S = decltype(stc)::value;
         constexpr int P = decltype(par)::value;
-        bf16x8 wk[2][2];  // [ks & 1][block]
+        bf16x8 wk[2][CB];  // [ks & 1][block]
         bf16x8 xf[2][FM];
         auto widen_ks = [&](auto kc) {
             constexpr int ks = decltype(kc)::value;
-            static_for<0, 2>([&](auto bc) {
+            static_for<0, CB>([&](auto bc) {
                 constexpr int b = decltype(bc)::value;
                 const u32x4 &r = raw[P][2 * b + (ks >> 1)];
                 wk[ks & 1][b] = widen8<WT>(r[2 * (ks & 1)], r[2 * (ks & 1) + 1]);
@@ -556,7 +563,7 @@ gemm_wd_kernel(const GemmArgs p) {
                 issue_w(t + NAS, std::integral_constant<int, P>{});
                 __builtin_amdgcn_sched_barrier(0);
             }
-            static_for<0, 2>([&](auto bc) {
+            static_for<0, CB>([&](auto bc) {
                 constexpr int b = decltype(bc)::value;
                 static_for<0, FM>([&](auto bmc) {
                     constexpr int bm = decltype(bmc)::value;
@@ -589,10 +596,10 @@ gemm_wd_kernel(const GemmArgs p) {
             issue_w(t + 2, std::integral_constant<int, P>{});
             __builtin_amdgcn_sched_barrier(0);
             // W(t+1) must have landed before it is widened: the loads after it are this step's.
-            wait_vmcnt<A_PER_WAVE + 4>();
+            wait_vmcnt<A_PER_WAVE + WLD>();
             mfmas(std::integral_constant<int, P>{}, std::integral_constant<int, P>{}, std::integral_constant<int, 1 - P>{});
             __builtin_amdgcn_sched_barrier(0);
-            wait_vmcnt<4>();
+            wait_vmcnt<WLD>();
             step_barrier();
         }
     };
@@ -615,12 +622,13 @@ gemm_wd_kernel(const GemmArgs p) {
     // The scales and biases of the wave's columns, loaded once for all its row blocks; their latency
     // overlaps the wait below.
     const bool has_bias = p.bias != nullptr;
-    ColParams cp[2];
+    ColParams cp[CB];
     {
         const int n_out = GLU ? p.glu_half : p.N;
-        static_for<0, 2>([&](auto bc) {
+        static_for<0, CB>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
-            load_col_params(p, cp[b], GLU ? slab * 32 : slab * 64 + 32 * b, GLU && b == 1 ? p.glu_half : 0, n_out, lane);
+            load_col_params(p, cp[b], GLU ? slab * 32 : slab * 64 + 32 * (b0 + b), GLU && b == 1 ? p.glu_half : 0, n_out,
+                            lane);
         });
     }
     // Every wave's last (clamped) activation load has landed before any wave writes its epilogue
@@ -641,44 +649,48 @@ gemm_wd_kernel(const GemmArgs p) {
     uint8_t *region = lds + wave * REGION;
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
-        static_for<0, GLU ? 1 : 2>([&](auto bc) {
+        static_for<0, GLU ? 1 : CB>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
-            const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
+            const int col0 = GLU ? slab * 32 : slab * 64 + 32 * (b0 + b);
             if (col0 < n_out)
-                store_block<EPI, OUT>(p, acc[b][bm], cp[b], acc[GLU ? 1 : b][bm], cp[GLU ? 1 : b], has_bias, col0,
+                store_block<EPI, OUT>(p, acc[b][bm], cp[b], acc[GLU ? CB - 1 : b][bm], cp[GLU ? CB - 1 : b], has_bias, col0,
                                       m0 + 32 * bm, n_out, region, lane);
         });
     });
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2>
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2>
 hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
     p.tiles_m = (p.M + BM - 1) / BM;
     const int slabs = GLU ? (p.glu_half + 31) / 32 : (p.N + 63) / 64;
-    p.tiles_n = (slabs + NW - 1) / NW;
+    p.tiles_n = CB == 2 ? (slabs + NW - 1) / NW : (p.N + 32 * NW - 1) / (32 * NW);
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN, NAS>), dim3(blocks), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN, NAS, CB>), dim3(blocks), dim3(64 * NW), 0, stream,
+                       p);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int NAS = 2>
+template <int BM, int NW, int OCC, int WT, int WL, int NAS = 2, int CB = 2>
 hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) {
-    if (slab_epilogue_fits(p, epi, out))
+    if (CB == 1 && (epi == EPI_SILU_GLU || epi == EPI_SITU_GLU)) return hipErrorInvalidValue;
+    if (CB == 2 && slab_epilogue_fits(p, epi, out))
         return epi == EPI_GELU ? launch_wd<BM, NW, OCC, WT, WL, EPI_GELU, OUT_BF16, true, NAS>(p, stream)
                                : launch_wd<BM, NW, OCC, WT, WL, EPI_NONE, OUT_BF16, true, NAS>(p, stream);
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O, false, NAS>(p, stream);
+    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O, false, NAS, CB>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)
     SQ8_CASE(EPI_GELU, OUT_F32)
-    SQ8_CASE(EPI_SILU_GLU, OUT_BF16)
-    SQ8_CASE(EPI_SILU_GLU, OUT_F32)
-    SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
-    SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    if constexpr (CB == 2) {
+        SQ8_CASE(EPI_SILU_GLU, OUT_BF16)
+        SQ8_CASE(EPI_SILU_GLU, OUT_F32)
+        SQ8_CASE(EPI_SITU_GLU, OUT_BF16)
+        SQ8_CASE(EPI_SITU_GLU, OUT_F32)
+    }
     SQ8_CASE(EPI_RESIDUAL, OUT_F32)
 #undef SQ8_CASE
     return hipErrorInvalidValue;

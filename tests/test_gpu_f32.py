@@ -73,8 +73,8 @@ def test_rounded_route_misses_the_fp32_bar(gemm, orc):
     assert judge(orc, e.cpu().numpy(), x, q, False, s, b, "none", torch.float32) <= 1e-6
 
 
-KERNEL_KNOBS = {"main256": "256", "main224": "224", "main128": "128", "main64": "64", "main32": "32", "skinny64": "s64",
-                "skinny32": "s32"}
+KERNEL_KNOBS = {"main256": "256", "main224": "224", "main128": "128", "main64": "64", "main32": "32", "main64n": "64n",
+                "skinny64": "s64", "skinny32": "s32"}
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 64), (33, 320, 200), (130, 3072, 520), (300, 1024, 1000)],

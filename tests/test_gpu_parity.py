@@ -353,7 +353,7 @@ def test_packed_baseline_shapes(gemm, orc, case):
 
 # ---- every weight-direct kernel on the same problems ----------------------------------------------
 
-TILES = {"main128": "128", "main256": "256", "main224": "224", "skinny64": "s64", "skinny32": "s32"}
+TILES = {"main128": "128", "main256": "256", "main224": "224", "main64n": "64n", "skinny64": "s64", "skinny32": "s32"}
 KERNEL_SHAPES = [
     (1, 64, 64),       # one K step: three of the skinny kernel's four waves have none
     (33, 320, 200),    # 5 K steps (not a multiple of the 4 waves), ragged M and N
@@ -382,6 +382,7 @@ def test_each_kernel_on_the_same_problem(gemm, orc, tile_gemm, shape, fp8):
         # The main kernels: one MFMA sequence over K at every height.
         assert torch.equal(results[("main256", out)], results[("main128", out)])
         assert torch.equal(results[("main224", out)], results[("main128", out)])
+        assert torch.equal(results[("main64n", out)], results[("main128", out)])
 
 
 @pytest.mark.parametrize("epi", ["silu", "situ"])
@@ -455,19 +456,21 @@ def test_residual_product_is_product_then_residual(gemm, orc, m, layout, gated):
 @pytest.mark.parametrize("m,n,epi,out_dtype", [(1000, 3000, "gelu", torch.bfloat16), (333, 1536, "none", torch.float32),
                                                (512, 2048, "silu", torch.bfloat16)])
 def test_tile_heights_same_bits(gemm, orc, tile_gemm, m, n, epi, out_dtype):
-    """The weight-direct kernel in 128-, 64- and 32-row tiles (the product's choice by how many tiles
-    fill the CUs): every output the same bits whichever height computes it — each sum runs the same
-    MFMA sequence over K — on ragged shapes, and within the bars of the truth on sampled rows."""
+    """The weight-direct kernel in 128-, 64- and 32-row tiles and in 64 × 128 tiles of one 32-column block a
+    wave (the product's choice by how many tiles fill the CUs): every output the same bits whichever tile
+    computes it — each sum runs the same MFMA sequence over K — on ragged shapes, and within the bars of
+    the truth on sampled rows."""
     k = 512
     x, q, s, b = problem(orc, m, k, n, False, 31 + m)
     wp = gemm.pack(weight_tensor(q, False, "nk"), layout="nk", glu=epi == "silu")
     outs = {}
-    for tile in ("128", "64", "32"):
+    for tile in ("128", "64", "32", "64n"):
         y = tile_gemm(tile).product(bf16_dev(x), wp, dev(s), bias=dev(b), out_dtype=out_dtype,
                          epilogue={"gelu": "gelu_tanh", "none": None, "silu": "silu_glu"}[epi])
         torch.cuda.synchronize()
         outs[tile] = y.float().cpu().numpy()
     assert bitwise_equal(outs["64"], outs["128"]) == 0 and bitwise_equal(outs["32"], outs["128"]) == 0
+    assert bitwise_equal(outs["64n"], outs["128"]) == 0
     judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
 
 
