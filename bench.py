@@ -40,7 +40,7 @@ RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # 512 MiB copy), by (workload, weight layout), as measured by the rocprofv3 --pmc runs recorded in
 # profiles/ (gemm_w256_kernel_c1_up_int8_packed_gelu.md, short_m_skinny_kernel_and_short_tiles.md,
 # hbm_traffic_and_mfma_busy_by_workload.md).
-TRAFFIC_BYTES = {("c1_up", "packed"): 403.6e6, ("c2_skinny", "packed"): 47.47e6, ("c0", "packed"): 56.95e6,
+TRAFFIC_BYTES = {("c1_up", "packed"): 403.6e6, ("c2_skinny", "packed"): 34.89e6, ("c0", "packed"): 56.95e6,
                  ("skinny_m1", "packed"): 9.70e6, ("skinny_m16", "packed"): 10.53e6, ("skinny_m64", "packed"): 13.19e6,
                  ("c1_down", "packed"): 450.3e6, ("c2_qkv", "packed"): 415.5e6, ("c3_gate_up", "packed"): 716.4e6,
                  ("c3_down", "packed"): 367.5e6, ("c3_plain", "packed"): 479.0e6, ("c1_w8a8", "packed"): 472.3e6,
