@@ -8,7 +8,9 @@
 //
 // Tile BM × 64·NW, NW waves of 64 lanes; wave w computes all BM rows × its 64 virtual columns as
 // 2 × (BM/32) blocks of v_mfma_f32_32x32x16_bf16 (the code the first operand, the activation the
-// second: each lane ends with 4 consecutive output columns of a row).
+// second: each lane ends with 4 consecutive output columns of a row). With CB = 1 a wave owns one
+// 32-column block instead (tile BM × 32·NW): the activation rows then serve twice the columns per
+// workgroup and each wave widens half the codes per MFMA (the short-M tiles of C2's text stream).
 //
 // K order inside a 64-step: MFMA sub-step ks of lane half h (lanes 32h..32h+31) takes
 // k ∈ [32h + 8ks, 32h + 8ks + 8). Any fixed permutation of K inside the step gives the same sums;
