@@ -474,6 +474,33 @@ def test_tile_heights_same_bits(gemm, orc, tile_gemm, m, n, epi, out_dtype):
     judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
 
 
+@pytest.mark.parametrize("head_dim", [0, 64])
+def test_one_block_waves_qkv_and_residual(gemm, orc, tile_gemm, head_dim):
+    """The 64 × 128 tiles of one 32-column block a wave on the fused QKV split (row-major and head-major:
+    a block lies in one output and one head) and on the gated residual epilogue: the same bits as the
+    128-row tiles, the QKV outputs judged against the truth."""
+    m, k, d = 200, 1024, 192
+    x, q, s, b = problem(orc, m, k, 3 * d, False, 45 + head_dim)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    outs = {}
+    for tile in ("64n", "128"):
+        parts = tile_gemm(tile).product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
+        torch.cuda.synchronize()
+        outs[tile] = np.concatenate([(t.permute(1, 0, 2).reshape(m, d) if head_dim else t).float().cpu().numpy()
+                                     for t in parts], axis=1)
+    assert bitwise_equal(outs["64n"], outs["128"]) == 0
+    judge(orc, outs["64n"], x, q, False, s, b, "none", torch.bfloat16, rows=orc.sample_rows(m, 64))
+    stream = orc.normal_f32(46, (m, 3 * d), 0.0, 1.0)
+    gate = dev(orc.normal_f32(47, (3 * d,), 0.0, 0.5))
+    res = {}
+    for tile in ("64n", "128"):
+        got = dev(stream)
+        tile_gemm(tile).product_residual(got, bf16_dev(x), w, dev(s), bias=dev(b), gate=gate)
+        torch.cuda.synchronize()
+        res[tile] = got.cpu().numpy()
+    assert bitwise_equal(res["64n"], res["128"]) == 0
+
+
 def test_streams_switched_between_products(gemm, orc):
     """Products on fp32 activations (each rounded into the context's scratch) on two streams in turn: the
     switch waits for the work queued on the previous stream, so each product reads its own operand."""
