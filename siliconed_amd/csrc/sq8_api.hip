@@ -729,7 +729,7 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
     ctx->wd_tile = knob(getenv("SQ8_TILE"), {{"256", sq8::WD_256}, {"224", sq8::WD_224}, {"128", sq8::WD_128}, {"64", sq8::WD_64},
-                                             {"32", sq8::WD_32}, {"64n", sq8::WD_64N}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32}});
+                                             {"32", sq8::WD_32}, {"64n", sq8::WD_64N}, {"64x192", sq8::WD_64x192}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32}});
     ctx->q8_tile = knob(getenv("SQ8_Q8_TILE"), {{"256", sq8::BL_64x256}, {"512", sq8::BL_64x512},
                                                 {"128x256", sq8::BL_128x256}, {"128x128", sq8::BL_128x128}});
     const char *splits = getenv("SQ8_SPLITS");

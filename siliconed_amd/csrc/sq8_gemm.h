@@ -49,10 +49,10 @@ hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, i
 // The weight-direct kernels (sq8_wdirect_inst.hip): [N, K] or packed weights, K a multiple of 64,
 // A aligned for 16-byte loads. `tile`: WD_256 (256 × 256, one workgroup per CU), WD_224 (224 × 256, the
 // same kernel), WD_128 (128 × 256, two workgroups per CU), WD_64 (64 × 256, one per CU), WD_32 (32 × 256,
-// two per CU), WD_64N (64 × 128, a 32-column block a wave, two per CU; not GLU), or the skinny-M kernel with
-// 64- or 32-row tiles of one 64-column slab and the K steps split over four waves (WD_SKINNY64,
-// WD_SKINNY32).
-enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 4, WD_32 = 5, WD_224 = 6, WD_64N = 7 };
+// two per CU), WD_64N (64 × 128, a 32-column block a wave, two per CU; not GLU), WD_64x192 (64 × 192, six
+// waves of one 32-column block; not GLU), or the skinny-M kernel with 64- or 32-row tiles of one 64-column
+// slab and the K steps split over four waves (WD_SKINNY64, WD_SKINNY32).
+enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 4, WD_32 = 5, WD_224 = 6, WD_64N = 7, WD_64x192 = 8 };
 // The tile for an M × N product (GLU: N = 2h): 256 or 224 rows × 256 while those tiles occupy more than
 // half the 256 CUs (the height whose rounds of 256 tiles cover the fewest rows; launch_wdirect takes
 // 128-row tiles where that kernel cannot serve the product), else the tallest of 128, 64 and 32 rows

@@ -42,7 +42,15 @@ int choose_wd_tile(int M, int N, bool glu) {
         return rows(224) < rows(256) ? WD_224 : WD_256;
     }
     if (tiles(128) >= 144) return WD_128;
-    if (tiles(64) >= 144) return WD_64;
+    if (tiles(64) >= 144) {
+        // 64 × 192 tiles of six one-block waves while they fit one round on the 256 CUs (and not for the GLU
+        // epilogues): less activation and weight per workgroup for the same rows. Measured against the 64-row
+        // tiles at K = 3072 in one process: C0 (1024 × 3072) 29.7 against 30.9 µs, and 3–5 % faster on five
+        // other shapes of one round (768 × 3072, 192 and 256 × 12288, 256 × 9216); past one round (1280 × 3072,
+        // 384 × 9216) 1.6× slower, so not there.
+        const long tiles64x192 = (long)((M + 63) / 64) * ((N + 191) / 192);
+        return !glu && tiles64x192 <= 256 ? WD_64x192 : WD_64;
+    }
     if (tiles(32) >= 144) {
         // 64 × 128 tiles, a 32-column block a wave (half the codes widened per MFMA), where they add no tiles
         // to the 32-row ones (a ragged last row tile would): measured over 15 shapes at K = 3072 in one

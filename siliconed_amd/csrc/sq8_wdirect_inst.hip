@@ -23,6 +23,11 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
         tile = WD_128;
     }
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile == WD_64x192) {
+        // Six waves of one 32-column block each: not for the GLU epilogues.
+        if (p.glu_half == 0) return wd::dispatch_wd<64, 6, 2, SQ8_WT, SQ8_WL, 2, 1>(p, epi, out, stream);
+        tile = WD_64;
+    }
     if (tile == WD_64) return wd::dispatch_wd<64, 4, 1, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_64N) {
         // One 32-column block a wave: not for the GLU epilogues (a wave needs both halves' blocks).

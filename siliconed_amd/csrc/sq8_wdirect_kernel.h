@@ -372,11 +372,13 @@ gemm_wd_kernel(const GemmArgs p) {
     constexpr int FM = BM / 32;                      // 32-row blocks per wave
     constexpr int SA = BM * 128;                     // bytes per A stage
     constexpr int A_BLOCKS = BM / 8;                 // 1 KB (8-row) blocks per A stage
-    constexpr int A_PER_WAVE = A_BLOCKS / NW;
+    // Activation blocks a wave loads per stage; when the waves outnumber an even split (six waves, eight
+    // blocks) the last loads of some waves repeat one of their own blocks, so every wave issues the same
+    // count (one vmcnt value fits them all) and each LDS block is written with the same bytes.
+    constexpr int A_PER_WAVE = (A_BLOCKS + NW - 1) / NW;
     constexpr int WLD = 2 * CB;                      // 16-byte weight loads per lane per K step
     static_assert(CB == 2 || (CB == 1 && !GLU && !LEAN && OCC == 2), "one-block waves: no GLU, block epilogue");
     // Every wave issues the same number of activation loads, so one vmcnt value fits them all.
-    static_assert(A_BLOCKS % NW == 0, "the activation blocks split evenly over the waves");
     static_assert(A_PER_WAVE + WLD < 64, "vmcnt budget");
     constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);  // epilogue bytes per wave
     // The epilogue regions lie over the A stages (both idle by then); short tiles need more than the stages.
@@ -406,9 +408,12 @@ gemm_wd_kernel(const GemmArgs p) {
 
     // ---- activation loads: wave block b = wave + NW·i, lane → row 8b + (lane>>3), chunk lane&7 ----
     uint32_t a_goff[A_PER_WAVE];
+    int a_blk[A_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < A_PER_WAVE; ++i) {
-        const int b = wave + NW * i;
+        int b = wave + NW * i;
+        if constexpr (A_BLOCKS % NW != 0) b = b < A_BLOCKS ? b : b - NW;
+        a_blk[i] = b;
         const int r = 8 * b + (lane >> 3);
         const int lc = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
         const int row = min(m0 + r, p.M - 1);
@@ -419,8 +424,8 @@ gemm_wd_kernel(const GemmArgs p) {
         const kern::gbytes base = Ag + (uint32_t)min(t, KT - 1) * (BK * 2);
 #pragma unroll
         for (int i = 0; i < A_PER_WAVE; ++i)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + (wave + NW * i) * 1024),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + a_blk[i] * 1024), 16, 0,
+                                             0);
     };
 
     // ---- weight loads: WLD × 16 bytes per lane per K step (load j: block b0 + j ÷ 2, half j & 1) ------

@@ -353,7 +353,8 @@ def test_packed_baseline_shapes(gemm, orc, case):
 
 # ---- every weight-direct kernel on the same problems ----------------------------------------------
 
-TILES = {"main128": "128", "main256": "256", "main224": "224", "main64n": "64n", "skinny64": "s64", "skinny32": "s32"}
+TILES = {"main128": "128", "main256": "256", "main224": "224", "main64n": "64n", "main64x192": "64x192",
+         "skinny64": "s64", "skinny32": "s32"}
 KERNEL_SHAPES = [
     (1, 64, 64),       # one K step: three of the skinny kernel's four waves have none
     (33, 320, 200),    # 5 K steps (not a multiple of the 4 waves), ragged M and N
@@ -383,6 +384,7 @@ def test_each_kernel_on_the_same_problem(gemm, orc, tile_gemm, shape, fp8):
         assert torch.equal(results[("main256", out)], results[("main128", out)])
         assert torch.equal(results[("main224", out)], results[("main128", out)])
         assert torch.equal(results[("main64n", out)], results[("main128", out)])
+        assert torch.equal(results[("main64x192", out)], results[("main128", out)])
 
 
 @pytest.mark.parametrize("epi", ["silu", "situ"])
@@ -464,41 +466,41 @@ def test_tile_heights_same_bits(gemm, orc, tile_gemm, m, n, epi, out_dtype):
     x, q, s, b = problem(orc, m, k, n, False, 31 + m)
     wp = gemm.pack(weight_tensor(q, False, "nk"), layout="nk", glu=epi == "silu")
     outs = {}
-    for tile in ("128", "64", "32", "64n"):
+    for tile in ("128", "64", "32", "64n", "64x192"):
         y = tile_gemm(tile).product(bf16_dev(x), wp, dev(s), bias=dev(b), out_dtype=out_dtype,
                          epilogue={"gelu": "gelu_tanh", "none": None, "silu": "silu_glu"}[epi])
         torch.cuda.synchronize()
         outs[tile] = y.float().cpu().numpy()
     assert bitwise_equal(outs["64"], outs["128"]) == 0 and bitwise_equal(outs["32"], outs["128"]) == 0
-    assert bitwise_equal(outs["64n"], outs["128"]) == 0
+    assert bitwise_equal(outs["64n"], outs["128"]) == 0 and bitwise_equal(outs["64x192"], outs["128"]) == 0
     judge(orc, outs["32"], x, q, False, s, b, epi, out_dtype, rows=orc.sample_rows(m, 64))
 
 
 @pytest.mark.parametrize("head_dim", [0, 64])
 def test_one_block_waves_qkv_and_residual(gemm, orc, tile_gemm, head_dim):
-    """The 64 × 128 tiles of one 32-column block a wave on the fused QKV split (row-major and head-major:
+    """The 64 × 128 and 64 × 192 tiles of one 32-column block a wave on the fused QKV split (row-major and head-major:
     a block lies in one output and one head) and on the gated residual epilogue: the same bits as the
     128-row tiles, the QKV outputs judged against the truth."""
     m, k, d = 200, 1024, 192
     x, q, s, b = problem(orc, m, k, 3 * d, False, 45 + head_dim)
     w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
     outs = {}
-    for tile in ("64n", "128"):
+    for tile in ("64n", "64x192", "128"):
         parts = tile_gemm(tile).product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
         torch.cuda.synchronize()
         outs[tile] = np.concatenate([(t.permute(1, 0, 2).reshape(m, d) if head_dim else t).float().cpu().numpy()
                                      for t in parts], axis=1)
-    assert bitwise_equal(outs["64n"], outs["128"]) == 0
+    assert bitwise_equal(outs["64n"], outs["128"]) == 0 and bitwise_equal(outs["64x192"], outs["128"]) == 0
     judge(orc, outs["64n"], x, q, False, s, b, "none", torch.bfloat16, rows=orc.sample_rows(m, 64))
     stream = orc.normal_f32(46, (m, 3 * d), 0.0, 1.0)
     gate = dev(orc.normal_f32(47, (3 * d,), 0.0, 0.5))
     res = {}
-    for tile in ("64n", "128"):
+    for tile in ("64n", "64x192", "128"):
         got = dev(stream)
         tile_gemm(tile).product_residual(got, bf16_dev(x), w, dev(s), bias=dev(b), gate=gate)
         torch.cuda.synchronize()
         res[tile] = got.cpu().numpy()
-    assert bitwise_equal(res["64n"], res["128"]) == 0
+    assert bitwise_equal(res["64n"], res["128"]) == 0 and bitwise_equal(res["64x192"], res["128"]) == 0
 
 
 def test_streams_switched_between_products(gemm, orc):
