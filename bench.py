@@ -332,6 +332,9 @@ def main() -> int:
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--shape", metavar="MxKxN", default=None,
+                    help="the workload's product at another M, K, N (same weight type, epilogue and inputs' "
+                         "distributions); the line then carries no measured traffic")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of the product, copy MIB MiB device→device --steps times (the known-size kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -357,6 +360,12 @@ def main() -> int:
 
     if args.workload in ("c4_block", "c4_block_w8a8"):
         return dit_block(args)
+    if args.shape:
+        m_, k_, n_ = (int(v) for v in args.shape.lower().split("x"))
+        w_ = list(WORKLOADS[args.workload])
+        w_[0:3] = [m_, k_, n_]
+        w_[6] = f"{w_[6]} (at {m_} x {k_} x {n_})"
+        WORKLOADS[args.workload] = tuple(w_)
     M, K, N, wt, epi, _, desc = WORKLOADS[args.workload]
     fp8 = wt == "fp8"
     q8 = wt == "q8_0"
@@ -498,7 +507,8 @@ def main() -> int:
     else:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
-    roofline.update({"traffic": TRAFFIC_BYTES.get((args.workload, args.layout)), "algorithmic_bytes": algo_bytes,
+    roofline.update({"traffic": None if args.shape else TRAFFIC_BYTES.get((args.workload, args.layout)),
+                     "algorithmic_bytes": algo_bytes,
                      "flops": flops, "intensity_flop_per_byte": round(intensity, 1),
                      "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5),
                      "mfma_bound_ms": round(flops / (peak_mfma * 1e12) * 1e3, 5)})
