@@ -1,0 +1,54 @@
+"""The product's own tile choice, on a seeded sweep of shapes around the rule's boundaries, on an MI355X.
+
+Every tile of the weight-direct main kernels (256- and 224-row tiles, 128/64/32-row tiles of 64-column
+waves, 64 × 128 and 64 × 192 tiles of one-block waves) runs one MFMA sequence over K, so whatever the
+rule picks among them gives the bits of the 128-row tiles; the skinny kernel splits K over its waves and
+gives the bits of its own 32-row tiles. So the default product equals one of those two bit for bit, and
+is judged against the oracle's fp64 truth on sampled rows at the reference's bars (Diagnostic.swift:105-107,
+DiagnosticProbes.swift:75-82).
+"""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from refgen import bitwise_equal
+from test_gpu_parity import bf16_dev, dev, judge, problem, weight_tensor
+
+pytestmark = pytest.mark.gpu
+
+_NAMES = {"none": None, "gelu": "gelu_tanh", "silu": "silu_glu"}
+
+
+def _case(i):
+    rng = random.Random(4100 + i)
+    k = 64 * rng.choice([1, 3, 8, 16, 48])
+    # Rows and columns on both sides of the rule's boundaries (tile counts 128, 144, 256 at the heights).
+    m = rng.choice([1, 17, 64, 100, 129, 256, 353, 400, 512, 704, 705, 1024, 1280, 1408, 1500, 2048, 4100])
+    n = rng.choice([64, 192, 320, 1024, 1344, 2880, 3000, 3072, 4608, 6144, 9216, 12288])
+    epi = rng.choice(["none", "gelu", "gelu", "silu"])
+    if epi == "silu" and n % 64:
+        n += 64 - n % 64
+    out = rng.choice([torch.bfloat16, torch.float32])
+    fp8 = rng.random() < 0.25
+    layout = rng.choice(["packed", "nk"])
+    return m, k, n, epi, out, fp8, layout
+
+
+@pytest.mark.parametrize("i", range(80))
+def test_default_tile_matches_a_fixed_tile(gemm, orc, tile_gemm, i):
+    m, k, n, epi, out, fp8, layout = _case(i)
+    print(f"tile rule case {i}: m {m} k {k} n {n} {epi} {out} fp8 {fp8} {layout}", flush=True)
+    x, q, s, b = problem(orc, m, k, n, fp8, 4200 + i)
+    w = weight_tensor(q, fp8, "nk")
+    if layout == "packed":
+        w = gemm.pack(w, layout="nk", glu=epi == "silu")
+    ys = {}
+    for name, g in (("default", gemm), ("128", tile_gemm("128")), ("s32", tile_gemm("s32"))):
+        y = g.product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), epilogue=_NAMES[epi], out_dtype=out)
+        torch.cuda.synchronize()
+        ys[name] = y.float().cpu().numpy()
+    assert bitwise_equal(ys["default"], ys["128"]) == 0 or bitwise_equal(ys["default"], ys["s32"]) == 0
+    if m >= 31:
+        judge(orc, ys["default"], x, q, fp8, s, b, epi, out, rows=orc.sample_rows(m, 32))
