@@ -68,11 +68,26 @@ def _compile(item) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every source and links the library; returns its path. Always recompiles."""
+def _stale(item) -> bool:
+    """True when the object is missing or older than its source or any header it may include."""
+    src, name, _ = item
+    obj = os.path.join(OBJ, name + ".o")
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(d, f) for d in (CSRC, os.path.join(ROOT, "include"))
+                                         for f in os.listdir(d) if f.endswith(".h")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compiles the sources and links the library; returns its path. Always recompiles every source,
+    unless `incremental` (then only those whose object is older than the source or a header)."""
     os.makedirs(OBJ, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(_compile, SOURCES))
+    todo = [it for it in SOURCES if _stale(it)] if incremental else SOURCES
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(len(todo), 1)) as pool:
+        list(pool.map(_compile, todo))
+    objs = [os.path.join(OBJ, name + ".o") for _, name, _ in SOURCES]
     tmp = LIB + ".tmp"
     # rocBLAS: the bf16-weight product's plain GEMM.
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lrocblas", "-o", tmp]
@@ -86,4 +101,4 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])

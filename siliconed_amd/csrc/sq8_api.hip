@@ -154,25 +154,40 @@ struct Product {
 
 // The fp32 route's operand (the reference's `submit` on an fp32 A, TensorGEMM.swift:296-360): A [m, k] —
 // rotated first by `group` in fp32 when non-zero (rotate_groups, TensorGEMM.swift:334-345) — split into its
-// three bf16 parts hi | mid | lo along K ([m, 3k], hi + mid + lo = x), in the context's scratch: the parts
-// first, the rotated rows after them.
-int stage_parts(sq8_ctx *ctx, const float *a, int64_t lda, int group, int m, int k, const uint16_t **out) {
+// three bf16 parts hi | mid | lo along K ([m, 3kp], hi + mid + lo = x, each part kp ≥ k wide with columns
+// [k, kp) zero), in the context's scratch: the parts first, the rotated rows after them.
+int stage_parts(sq8_ctx *ctx, const float *a, int64_t lda, int group, int m, int k, int kp, const uint16_t **out) {
     const size_t mk = (size_t)m * (size_t)k;
-    const size_t bytes = mk * 6 + (group != 0 ? mk * 4 : 0);
+    const size_t parts = (size_t)m * (size_t)kp * 6;
+    const size_t bytes = parts + (group != 0 ? mk * 4 : 0);
     int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
     if (st != SQ8_OK) return st;
     uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
     const float *src = a;
     int64_t lds = lda;
     if (group != 0) {
-        // mk·6 bytes in: a multiple of 4 as k is even.
-        float *r = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + mk * 6);
+        // m·kp·6 bytes in: a multiple of 4 as kp is even.
+        float *r = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + parts);
         hipError_t e = sq8::launch_rotate_groups(a, false, lda, r, false, k, m, k, group, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
         src = r;
         lds = k;
     }
-    hipError_t e = sq8::launch_split3(src, lds, y, m, k, ctx->stream);
+    hipError_t e = sq8::launch_split3(src, lds, y, m, k, kp, ctx->stream);
+    if (e != hipSuccess) return hip_status(e);
+    *out = y;
+    return SQ8_OK;
+}
+
+// A bf16 operand for the step kernels when K is not a whole number of 64-wide steps: rows copied into the
+// context's scratch kp = ⌈k/64⌉·64 apart with columns [k, kp) zero (zero products with the packed
+// weight's zero codes past K: every sum as over k alone).
+int stage_padded_bf16(sq8_ctx *ctx, const uint16_t *a, int64_t lda, int m, int k, int kp, const uint16_t **out) {
+    const size_t bytes = (size_t)m * (size_t)kp * 2;
+    int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
+    if (st != SQ8_OK) return st;
+    uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
+    hipError_t e = sq8::launch_pad_bf16_rows(a, lda, y, m, k, kp, ctx->stream);
     if (e != hipSuccess) return hip_status(e);
     *out = y;
     return SQ8_OK;
@@ -192,14 +207,20 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     if (!is_packed(q.w_layout) && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
     if (q.split == 0 && q.head_dim == 0 && q.ldc < n_out) return SQ8_EINVAL;
     if (q.group != 0 && (!sq8::is_rotation_group(q.group) || q.k % q.group != 0)) return SQ8_EINVAL;
-    if (q.residual && (q.c_dtype != SQ8_F32 || is_glu(q.epilogue) || q.k % 64 != 0)) return SQ8_EUNSUPPORTED;
+    if (q.residual && (q.c_dtype != SQ8_F32 || is_glu(q.epilogue))) return SQ8_EUNSUPPORTED;
     if (q.exact && q.a_dtype != SQ8_F32) return SQ8_EINVAL;
-    if (q.exact && q.k % 64 != 0) return SQ8_EUNSUPPORTED;  // the parts are whole K steps
+    // K not a whole number of 64-wide steps on the step kernels (a packed weight, the fp32 route, the
+    // residual epilogue): the operand is staged with its rows padded to kp (zeros past k) and the weight
+    // packed (zero codes past k), so each sum is the one over k alone (TensorGEMM.swift:124-135 computes
+    // any K). The bf16 route on codes as they lie keeps the guarded kernel for such K.
+    const int kp = (q.k + 63) / 64 * 64;
+    const bool pad_k = q.k % 64 != 0 && (q.exact || q.residual || is_packed(q.w_layout));
     // The kernels address A and W with 32-bit byte offsets from their bases.
-    if ((int64_t)q.m * (q.exact ? 3 * (int64_t)q.k : q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k) * 2 >
-            (int64_t)UINT32_MAX ||
-        (is_packed(q.w_layout) ? sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue))
-                               : (int64_t)(q.w_layout == SQ8_KN ? q.k : q.n) * q.ldw) > (int64_t)UINT32_MAX)
+    const int64_t a_row = q.exact ? 3 * (int64_t)kp : pad_k ? kp : q.a_dtype == SQ8_BF16 && q.group == 0 ? q.lda : q.k;
+    if ((int64_t)q.m * a_row * 2 > (int64_t)UINT32_MAX ||
+        std::max<int64_t>(sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue)),
+                          is_packed(q.w_layout) ? 0 : (int64_t)(q.w_layout == SQ8_KN ? q.k : q.n) * q.ldw) >
+            (int64_t)UINT32_MAX)
         return SQ8_EUNSUPPORTED;
 
     DeviceScope scope(ctx->device);
@@ -217,33 +238,43 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         // The fp32 route: the kernels run K' = 3K steps against the weight's K steps, each part facing
         // the whole weight, so every product is exact and the sums are fp32.
         const uint16_t *y = nullptr;
-        st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, q.group, q.m, q.k, &y);
+        st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, q.group, q.m, q.k, kp, &y);
         if (st != SQ8_OK) return st;
         p.a = y;
-        p.lda = 3 * (int64_t)q.k;
+        p.lda = 3 * (int64_t)kp;
     } else if (q.group != 0) {
         // convrot: the operand rotated (fp32 butterflies) and rounded to bf16 in one pass, into the
-        // context's scratch (TensorGEMMBF16.swift:222-233: rotate_groups, then round_bf16).
-        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        // context's scratch (TensorGEMMBF16.swift:222-233: rotate_groups, then round_bf16); rows kp apart
+        // with zero columns past k when K is padded.
+        const int ky = pad_k ? kp : q.k;
+        const size_t bytes = (size_t)q.m * (size_t)ky * 2;
         st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
         if (st != SQ8_OK) return st;
         uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
-        hipError_t e = sq8::launch_rotate_groups(q.a, q.a_dtype == SQ8_BF16, q.lda, y, true, q.k, q.m, q.k, q.group,
+        hipError_t e = sq8::launch_rotate_groups(q.a, q.a_dtype == SQ8_BF16, q.lda, y, true, ky, q.m, q.k, q.group,
                                                  ctx->stream);
+        if (e == hipSuccess) e = sq8::launch_zero_tail(y, ky, q.m, q.k, ky, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
         p.a = y;
-        p.lda = q.k;
+        p.lda = ky;
     } else if (q.a_dtype == SQ8_F32) {
         // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
-        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        const int ky = pad_k ? kp : q.k;
+        const size_t bytes = (size_t)q.m * (size_t)ky * 2;
         st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
         if (st != SQ8_OK) return st;
         const float *x = static_cast<const float *>(q.a);
         uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
-        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, ctx->stream);
+        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, ky, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
         p.a = y;
-        p.lda = q.k;
+        p.lda = ky;
+    } else if (pad_k) {
+        const uint16_t *y = nullptr;
+        st = stage_padded_bf16(ctx, static_cast<const uint16_t *>(q.a), q.lda, q.m, q.k, kp, &y);
+        if (st != SQ8_OK) return st;
+        p.a = y;
+        p.lda = kp;
     }
     p.w = static_cast<const uint8_t *>(q.w);
     p.ldw = q.ldw;
@@ -290,7 +321,8 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     const int wt = q.w_dtype == SQ8_INT8 ? sq8::W_INT8 : sq8::W_FP8;
     const int out = q.c_dtype == SQ8_F32 ? sq8::OUT_F32 : sq8::OUT_BF16;
     const int cols_per_half = is_glu(q.epilogue) ? q.n / 2 : q.n;
-    const bool k_steps = q.k > 0 && (q.k % 64) == 0;
+    // Whole 64-wide K steps: K itself, or K padded in the staging above.
+    const bool k_steps = q.k > 0 && ((q.k % 64) == 0 || pad_k);
     p.kt = (q.k + 63) / 64;
     if (q.exact) {
         p.kt_w = p.kt;  // the weight's steps; the activation has three parts of them
@@ -303,13 +335,15 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     // The fp32 route and the residual epilogue run on the weight-direct kernels only: they repack any
     // [K, N] weight (the general pack where the fast one does not apply).
     int wl_run = q.w_layout;
-    if (q.w_layout == SQ8_KN && p.a_vec && k_steps &&
-        (q.exact || q.residual || sq8::pack_is_fast(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue)))) {
+    // A padded K takes the packed layout (its zero codes past k) whatever the weight's own layout.
+    if (!is_packed(q.w_layout) && p.a_vec && k_steps &&
+        (pad_k || (q.w_layout == SQ8_KN && (q.exact || q.residual ||
+                                            sq8::pack_is_fast(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue)))))) {
         const int64_t bytes = sq8::packed_bytes(q.k, q.n, is_glu(q.epilogue));
         st = reserve_buffer(ctx, &ctx->wpack, &ctx->wpack_bytes, (size_t)bytes);
         if (st != SQ8_OK) return st;
-        e = sq8::launch_pack(p.w, sq8::W_KN, p.ldw, q.k, q.n, is_glu(q.epilogue), static_cast<uint8_t *>(ctx->wpack),
-                             ctx->stream);
+        e = sq8::launch_pack(p.w, q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK, p.ldw, q.k, q.n, is_glu(q.epilogue),
+                             static_cast<uint8_t *>(ctx->wpack), ctx->stream);
         if (e != hipSuccess) return hip_status(e);
         p.w = static_cast<const uint8_t *>(ctx->wpack);
         wl_run = is_glu(q.epilogue) ? SQ8_PACKED_GLU : SQ8_PACKED;
@@ -534,10 +568,16 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     if (!q.a || !q.w || !q.c || (!packed && !q.scale)) return SQ8_EINVAL;
     if (q.lda < q.k || q.ldc < n_out) return SQ8_EINVAL;
     if (!packed && q.ldw < (q.w_layout == SQ8_KN ? q.n : q.k)) return SQ8_EINVAL;
-    // Blocks of whole MFMA sub-steps, whole activation tiles, 32-bit offsets into A and the packed codes.
-    if (q.block % 32 != 0 || q.k % q.block != 0 || q.k % 64 != 0) return SQ8_EUNSUPPORTED;
+    // Blocks of whole MFMA sub-steps (32 rows of K), 32-bit offsets into A and the packed codes. K need not
+    // be a whole number of 64-wide steps (the reference computes every block, TensorGEMM.swift:143-171,
+    // `row < K` at :162): the operand is then staged with rows padded to kp, zeros past k, against the
+    // packed layout's zero codes and zero scales past k.
+    if (q.block % 32 != 0 || q.k % q.block != 0) return SQ8_EUNSUPPORTED;
     if (q.exact && q.a_dtype != SQ8_F32) return SQ8_EINVAL;
-    if ((int64_t)q.m * (q.exact ? 3 * (int64_t)q.k : q.a_dtype == SQ8_BF16 ? q.lda : q.k) * 2 > (int64_t)UINT32_MAX ||
+    const int kp = (q.k + 63) / 64 * 64;
+    const bool pad_k = q.k % 64 != 0;
+    const int64_t a_row = q.exact ? 3 * (int64_t)kp : pad_k ? kp : q.a_dtype == SQ8_BF16 ? q.lda : q.k;
+    if ((int64_t)q.m * a_row * 2 > (int64_t)UINT32_MAX ||
         sq8::packed_blocks_bytes(q.k, q.n, is_glu(q.epilogue)) > (int64_t)UINT32_MAX)
         return SQ8_EUNSUPPORTED;
     if (packed && !aligned(q.w, 16)) return SQ8_EINVAL;
@@ -555,21 +595,27 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     if (q.exact) {
         // The fp32 route (the reference's `blocks` pipeline on an fp32 A, TensorGEMM.swift:307-320).
         const uint16_t *y = nullptr;
-        int st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, 0, q.m, q.k, &y);
+        int st = stage_parts(ctx, static_cast<const float *>(q.a), q.lda, 0, q.m, q.k, kp, &y);
         if (st != SQ8_OK) return st;
         p.a = y;
-        p.lda = 3 * (int64_t)q.k;
+        p.lda = 3 * (int64_t)kp;
     } else if (q.a_dtype == SQ8_F32) {
         // The operand rounded to bf16 once, into the context's scratch (TensorGEMMBF16.swift:208-264).
-        const size_t bytes = (size_t)q.m * (size_t)q.k * 2;
+        const size_t bytes = (size_t)q.m * (size_t)kp * 2;
         int st = reserve_scratch(ctx, bytes > 0 ? bytes : 2);
         if (st != SQ8_OK) return st;
         const float *x = static_cast<const float *>(q.a);
         uint16_t *y = static_cast<uint16_t *>(ctx->scratch);
-        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, ctx->stream);
+        hipError_t e = sq8::launch_round_bf16_rows(x, q.lda, y, q.m, q.k, kp, ctx->stream);
         if (e != hipSuccess) return hip_status(e);
         p.a = y;
-        p.lda = q.k;
+        p.lda = kp;
+    } else if (pad_k) {
+        const uint16_t *y = nullptr;
+        int st = stage_padded_bf16(ctx, static_cast<const uint16_t *>(q.a), q.lda, q.m, q.k, kp, &y);
+        if (st != SQ8_OK) return st;
+        p.a = y;
+        p.lda = kp;
     }
     if (!aligned(p.a, 16) || (p.lda % 8) != 0) return SQ8_EUNSUPPORTED;
     p.w = static_cast<const uint8_t *>(q.w);
@@ -591,7 +637,7 @@ int run_blocks(sq8_ctx *ctx, const Blocks &q, double *gpu_seconds) {
     p.M = q.m;
     p.N = q.n;
     p.K = q.k;
-    p.kt = q.k / 64;
+    p.kt = kp / 64;
     if (q.exact) {
         p.kt_w = p.kt;  // the weight's steps; the activation has three parts of them
         p.kt = 3 * p.kt_w;
@@ -665,7 +711,7 @@ int run_bf16_weight(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, const
         int64_t ldp = lda;
         int count = 1;
         if (a_dtype == SQ8_F32) {
-            int st = stage_parts(ctx, static_cast<const float *>(a), lda, 0, m, k, &parts);
+            int st = stage_parts(ctx, static_cast<const float *>(a), lda, 0, m, k, k, &parts);
             if (st != SQ8_OK) return st;
             ldp = 3 * (int64_t)k;
             count = 3;

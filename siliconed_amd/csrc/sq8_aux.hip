@@ -52,40 +52,68 @@ __global__ void __launch_bounds__(256) round_bf16_kernel(const float *__restrict
         y[i] = (uint16_t)round_bf16(x[i]);
 }
 
-// The same rounding of `rows` rows of k values read `ldx` apart, written k apart (a strided fp32 operand
-// into the packed bf16 copy the products read).
+// The same rounding of `rows` rows of k values read `ldx` apart, written kp ≥ k apart with columns
+// [k, kp) zero (a strided fp32 operand into the bf16 copy the products read, padded to whole K steps).
 __global__ void __launch_bounds__(256) round_bf16_rows_kernel(const float *__restrict__ x, int64_t ldx,
-                                                              uint16_t *__restrict__ y, int64_t rows, int k) {
-    const int64_t count = rows * k;
+                                                              uint16_t *__restrict__ y, int64_t rows, int k, int kp) {
+    const int64_t count = rows * kp;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / k;
-        y[i] = (uint16_t)round_bf16(x[r * ldx + (i - r * k)]);
+        const int64_t r = i / kp;
+        const int c = (int)(i - r * kp);
+        y[i] = c < k ? (uint16_t)round_bf16(x[r * ldx + c]) : (uint16_t)0;
     }
 }
 
-// fp32 → three bf16 parts along K: y[r, k] = hi, y[r, K + k] = mid, y[r, 2K + k] = lo, each part the top
-// 16 bits of what the one before leaves (hi = x truncated to bf16, mid = (x − hi) truncated, lo = x − hi − mid):
-// 24 significant bits in three parts of 8, every difference exact, no part rounded, so hi + mid + lo = x and
-// every product of a part with a code is exact. Every part is a normal bf16 for |x| ≥ 2^−103; an infinity
-// or NaN is its hi part alone. One thread per value of row r, column k.
-__global__ void __launch_bounds__(256) split3_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ y,
-                                                     int64_t rows, int k) {
-    const int64_t count = rows * k;
+// bf16 rows copied as they are, k values read `ldx` apart, written kp ≥ k apart with columns [k, kp)
+// zero: a bf16 operand whose K is not a whole number of 64-wide steps, padded for the step kernels.
+__global__ void __launch_bounds__(256) pad_bf16_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                            uint16_t *__restrict__ y, int64_t rows, int k, int kp) {
+    const int64_t count = rows * kp;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / k;
-        const int c = (int)(i - r * k);
-        const float v = x[r * ldx + c];
-        const uint32_t u = __float_as_uint(v);
-        uint32_t m = 0, l = 0;
-        if ((u & 0x7f800000u) != 0x7f800000u) {
-            const float r1 = v - __uint_as_float(u & 0xffff0000u);  // the low 16 bits of x: exact
-            m = __float_as_uint(r1) >> 16;
-            l = __float_as_uint(r1 - __uint_as_float(m << 16)) >> 16;  // ≤ 8 bits left: a bf16 value
+        const int64_t r = i / kp;
+        const int c = (int)(i - r * kp);
+        y[i] = c < k ? x[r * ldx + c] : (uint16_t)0;
+    }
+}
+
+// Columns [k, kp) of `rows` bf16 rows `ld` apart set to zero (the padding after a pass that wrote
+// only the first k).
+__global__ void __launch_bounds__(256) zero_tail_kernel(uint16_t *__restrict__ y, int64_t ld, int64_t rows, int k,
+                                                        int kp) {
+    const int w = kp - k;
+    const int64_t count = rows * w;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / w;
+        y[r * ld + k + (i - r * w)] = 0;
+    }
+}
+
+// fp32 → three bf16 parts along K: y[r, c] = hi, y[r, kp + c] = mid, y[r, 2kp + c] = lo (kp ≥ k; columns
+// [k, kp) of each part zero, the padding to whole K steps), each part the top 16 bits of what the one
+// before leaves (hi = x truncated to bf16, mid = (x − hi) truncated, lo = x − hi − mid): 24 significant
+// bits in three parts of 8, every difference exact, no part rounded, so hi + mid + lo = x and every
+// product of a part with a code is exact. Every part is a normal bf16 for |x| ≥ 2^−103; an infinity or
+// NaN is its hi part alone. One thread per value of row r, column c.
+__global__ void __launch_bounds__(256) split3_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ y,
+                                                     int64_t rows, int k, int kp) {
+    const int64_t count = rows * kp;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / kp;
+        const int c = (int)(i - r * kp);
+        uint32_t u = 0, m = 0, l = 0;
+        if (c < k) {
+            const float v = x[r * ldx + c];
+            u = __float_as_uint(v);
+            if ((u & 0x7f800000u) != 0x7f800000u) {
+                const float r1 = v - __uint_as_float(u & 0xffff0000u);  // the low 16 bits of x: exact
+                m = __float_as_uint(r1) >> 16;
+                l = __float_as_uint(r1 - __uint_as_float(m << 16)) >> 16;  // ≤ 8 bits left: a bf16 value
+            }
         }
-        uint16_t *row = y + r * 3 * (int64_t)k;
+        uint16_t *row = y + r * 3 * (int64_t)kp;
         row[c] = (uint16_t)(u >> 16);
-        row[k + c] = (uint16_t)m;
-        row[2 * k + c] = (uint16_t)l;
+        row[kp + c] = (uint16_t)m;
+        row[2 * kp + c] = (uint16_t)l;
     }
 }
 
@@ -220,10 +248,10 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
     return hipGetLastError();
 }
 
-hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream) {
-    const int64_t count = rows * k;
+hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp, hipStream_t stream) {
+    const int64_t count = rows * kp;
     if (count == 0) return hipSuccess;
-    hipLaunchKernelGGL(split3_kernel, dim3(grid_for(count)), dim3(256), 0, stream, x, ldx, y, rows, k);
+    hipLaunchKernelGGL(split3_kernel, dim3(grid_for(count)), dim3(256), 0, stream, x, ldx, y, rows, k, kp);
     return hipGetLastError();
 }
 
@@ -233,10 +261,24 @@ hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStre
     return hipGetLastError();
 }
 
-hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream) {
-    if (rows == 0 || k == 0) return hipSuccess;
-    if (ldx == k) return launch_round_bf16(x, y, rows * k, stream);
-    hipLaunchKernelGGL(round_bf16_rows_kernel, dim3(grid_for(rows * k)), dim3(256), 0, stream, x, ldx, y, rows, k);
+hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp,
+                                  hipStream_t stream) {
+    if (rows == 0 || kp == 0) return hipSuccess;
+    if (ldx == k && kp == k) return launch_round_bf16(x, y, rows * k, stream);
+    hipLaunchKernelGGL(round_bf16_rows_kernel, dim3(grid_for(rows * kp)), dim3(256), 0, stream, x, ldx, y, rows, k, kp);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad_bf16_rows(const uint16_t *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp,
+                                hipStream_t stream) {
+    if (rows == 0 || kp == 0) return hipSuccess;
+    hipLaunchKernelGGL(pad_bf16_rows_kernel, dim3(grid_for(rows * kp)), dim3(256), 0, stream, x, ldx, y, rows, k, kp);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_tail(uint16_t *y, int64_t ld, int64_t rows, int k, int kp, hipStream_t stream) {
+    if (rows == 0 || kp <= k) return hipSuccess;
+    hipLaunchKernelGGL(zero_tail_kernel, dim3(grid_for(rows * (kp - k))), dim3(256), 0, stream, y, ld, rows, k, kp);
     return hipGetLastError();
 }
 

@@ -89,12 +89,19 @@ hipError_t launch_dequantize(const uint8_t *codes, int wt, int64_t rows, int64_t
                              int scale_dtype, int scale_layout, int64_t block_rows, int64_t first_row, float *out,
                              hipStream_t stream);
 hipError_t launch_round_bf16(const float *x, uint16_t *y, int64_t count, hipStream_t stream);
-// rows × k values read ldx apart → rows × k bf16 written k apart (one launch, any stride).
-hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream);
-// fp32 [rows, k] (leading dimension ldx) → bf16 [rows, 3k]: the three parts hi | mid | lo of each value
-// (each the top 16 bits of what the one before leaves: hi + mid + lo = x, no part rounded), the fp32 route's
-// operand.
-hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, hipStream_t stream);
+// rows × k values read ldx apart → rows × kp bf16 written kp apart (kp ≥ k, columns [k, kp) zero; one
+// launch, any stride).
+hipError_t launch_round_bf16_rows(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp,
+                                  hipStream_t stream);
+// bf16 rows × k read ldx apart → rows × kp written kp apart, columns [k, kp) zero.
+hipError_t launch_pad_bf16_rows(const uint16_t *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp,
+                                hipStream_t stream);
+// Columns [k, kp) of rows × ld bf16 set to zero.
+hipError_t launch_zero_tail(uint16_t *y, int64_t ld, int64_t rows, int k, int kp, hipStream_t stream);
+// fp32 [rows, k] (leading dimension ldx) → bf16 [rows, 3kp]: the three parts hi | mid | lo of each value
+// (each the top 16 bits of what the one before leaves: hi + mid + lo = x, no part rounded), each part kp ≥ k
+// wide with columns [k, kp) zero; the fp32 route's operand.
+hipError_t launch_split3(const float *x, int64_t ldx, uint16_t *y, int64_t rows, int k, int kp, hipStream_t stream);
 
 // ComfyUI's convrot (sq8_convrot.hip): the activation's rotation x·R by groups of `group` (4, 16,
 // 64 or 256; k a multiple of it), fp32 or bf16 in, fp32 or bf16 (rounded to nearest even) out; and

@@ -101,6 +101,23 @@ def _row_major(t: torch.Tensor, what: str) -> int:
     return t.stride(0) if t.size(0) > 1 else max(t.size(1), 1)
 
 
+def _block_scales(scale: Optional[torch.Tensor], lay: int, n: int, k: int, block: int, ldw: int) -> None:
+    """Checks block scales against what the library reads: [n, k/block] contiguous for "nk" codes;
+    for "kn" codes [k/block, n] rows with the codes' own row stride `ldw` (scale[blk·ldw + col]: a
+    column-sliced weight w[:, :n] takes its scales as scale_full[:, :n])."""
+    want = (n, k // block) if lay == abi.NK else (k // block, n)
+    if scale is None or scale.dtype not in _SCALE_DTYPES or tuple(scale.shape) != want:
+        raise ValueError(f"scale must be fp32/bf16/fp16 {want}")
+    if lay == abi.NK:
+        if not scale.is_contiguous():
+            raise ValueError(f"scale must be contiguous {want}")
+        return
+    rows = want[0]
+    if rows > 0 and n > 0 and ((n > 1 and scale.stride(1) != 1) or (rows > 1 and scale.stride(0) != ldw)):
+        raise ValueError(f"scale {want} must have rows of stride {ldw}, the codes' row stride "
+                         f"(it has strides {tuple(scale.stride())})")
+
+
 class TensorGEMM:
     """One context (device + stream) of the library: `TensorGEMM` of the reference."""
 
@@ -434,9 +451,7 @@ class TensorGEMM:
         n, k = (w.shape[0], w.shape[1]) if lay == abi.NK else (w.shape[1], w.shape[0])
         if block <= 0 or k % block:
             raise ValueError(f"k = {k} is not a multiple of the block {block}")
-        want = (n, k // block) if lay == abi.NK else (k // block, n)
-        if scale.dtype not in _SCALE_DTYPES or tuple(scale.shape) != want or not scale.is_contiguous():
-            raise ValueError(f"scale must be contiguous fp32/bf16/fp16 {want}")
+        _block_scales(scale, lay, n, k, block, _row_major(w, "w"))
         size = abi.load().sq8_packed_blocks_bytes(k, n, int(glu))
         if size < 0:
             raise ValueError("a GLU weight has an even number of columns")
@@ -469,10 +484,9 @@ class TensorGEMM:
             n = w.shape[0] if lay == abi.NK else w.shape[1]
             if (w.shape[1] if lay == abi.NK else w.shape[0]) != k:
                 raise ValueError(f"x [{m}, {k}] and w {tuple(w.shape)} ({layout}) disagree on K")
-            want = (n, k // block) if lay == abi.NK else (k // block, n)
-            if scale is None or scale.dtype not in _SCALE_DTYPES or tuple(scale.shape) != want or \
-                    not scale.is_contiguous():
-                raise ValueError(f"scale must be contiguous fp32/bf16/fp16 {want}")
+            if block <= 0 or k % block:
+                raise ValueError(f"k = {k} is not a multiple of the block {block}")
+            _block_scales(scale, lay, n, k, block, _row_major(w, "w"))
             ldw, wptr, sptr, sdt = _row_major(w, "w"), _dev(w, "w"), _dev(scale, "scale"), _SCALE_DTYPES[scale.dtype]
         n_out = n // 2 if epi in (abi.EPI_SILU_GLU, abi.EPI_SITU_GLU) else n
         if out is None:

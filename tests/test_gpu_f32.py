@@ -195,12 +195,47 @@ def test_fp32_route_block_scales_reference_entry(gemm, orc):
           torch.float32, values=True)
 
 
+@pytest.mark.parametrize("k", [96, 160, 3072 + 32])
+@pytest.mark.parametrize("layout", ["nk", "kn", "packed"])
+def test_fp32_route_any_k(gemm, orc, k, layout):
+    """K not a multiple of 64 on the fp32 route (the reference's fp32 `linear_int8` has a dynamic K
+    extent, TensorGEMM.swift:124-135): the parts padded to whole steps with zeros, the weight packed
+    with zero codes past K; judged at the fp32 bar (1e-5), every epilogue, fp32 and bf16 outputs."""
+    m, n = 150, 192
+    for fp8 in (False, True):
+        x, q, s, b = f32_problem(orc, m, k, n, fp8, 900 + k)
+        for epi in ("none", "gelu", "silu"):
+            w = weight_tensor(q, fp8, "nk" if layout == "nk" else "kn")
+            if layout == "packed":
+                w = gemm.pack(w, layout="kn", glu=epi == "silu", fp8=fp8 or None)
+            for out in (torch.float32, torch.bfloat16):
+                y = gemm.product(dev(x), w, dev(s), layout="nk" if layout == "nk" else "kn", bias=dev(b),
+                                 epilogue=_NAMES[epi], out_dtype=out, rounding=False)
+                torch.cuda.synchronize()
+                judge(orc, y.float().cpu().numpy(), x, q, fp8, s, b, epi, out)
+
+
+@pytest.mark.parametrize("k", [96, 160, 3072 + 32])
+def test_fp32_route_block_scales_any_k(gemm, orc, k):
+    """Q8_0 (blocks of 32) on the fp32 route at K = 32·odd (the reference's `linear_q8` computes every
+    64-row chunk under `row < K`, TensorGEMM.swift:143-171, :162): against the fp64 truth at 1e-5."""
+    m, n, block = 130, 192, 32
+    x, q, d, b = _q8(orc, m, k, n, block, 950 + k)
+    for layout in ("nk", "kn"):
+        if layout == "nk":
+            w, sc = dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16)
+        else:
+            w, sc = dev(np.ascontiguousarray(q.T)).view(torch.int8), dev(np.ascontiguousarray(d.T).astype(np.float32))
+        for epi in ("none", "gelu"):
+            y = gemm.product_blocks(dev(x), w, sc, block, layout=layout, bias=dev(b), epilogue=_NAMES[epi],
+                                    out_dtype=torch.float32, rounding=False)
+            torch.cuda.synchronize()
+            judge(orc, y.cpu().numpy(), x, _q8_truth_weight(q, d, block), None, np.ones(n, np.float32), b, epi,
+                  torch.float32, values=True)
+
+
 def test_fp32_route_refusals(gemm, orc):
     from siliconed_amd import abi
-    x, q, s, b = f32_problem(orc, 8, 96, 64, False, 3)
-    with pytest.raises(abi.SQ8Error) as e:       # k not a multiple of 64: the parts are whole K steps
-        gemm.product(dev(x), weight_tensor(q, False, "nk"), dev(s), layout="nk", rounding=False)
-    assert e.value.status == abi.EUNSUPPORTED
     x, q, s, b = f32_problem(orc, 8, 128, 64, False, 3)
     lib = abi.load()
     w, sv, xt = weight_tensor(q, False, "nk"), dev(s), dev(x)

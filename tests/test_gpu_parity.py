@@ -455,6 +455,32 @@ def test_residual_product_is_product_then_residual(gemm, orc, m, layout, gated):
     assert bitwise_equal(got.cpu().numpy(), expect.cpu().numpy()) == 0
 
 
+@pytest.mark.parametrize("k", [96, 3072 + 32])
+def test_packed_and_residual_any_k(gemm, orc, k):
+    """K not a multiple of 64 on the step kernels (the reference's products take any K,
+    TensorGEMM.swift:124-135): a packed weight (zero codes past K) against an activation staged with its
+    rows padded by zeros, judged against the oracle; the gated residual on [N, K] codes of the same K
+    (repacked per product) bit-equal to that product followed by the residual pass."""
+    m, n = 300, 768
+    x_, q, s, b = problem(orc, m, k, n, False, k + 5)
+    w = weight_tensor(q, False, "nk")
+    wp = gemm.pack(w, layout="nk")
+    for epi, out in (("gelu", torch.bfloat16), ("none", torch.float32)):
+        y = gemm.product(bf16_dev(x_), wp, dev(s), bias=dev(b), epilogue=None if epi == "none" else "gelu_tanh",
+                         out_dtype=out)
+        torch.cuda.synchronize()
+        judge(orc, y.float().cpu().numpy(), x_, q, False, s, b, epi, out)
+    y = gemm.product(bf16_dev(x_), wp, dev(s), bias=dev(b), out_dtype=torch.float32)
+    stream = orc.normal_f32(k + 9, (m, n), 0.0, 1.0)
+    gate = dev(orc.normal_f32(k + 10, (n,), 0.0, 0.5))
+    expect = dev(stream)
+    gemm.gated_residual(expect, y, gate)
+    got = dev(stream)
+    gemm.product_residual(got, bf16_dev(x_), w, dev(s), layout="nk", bias=dev(b), gate=gate)
+    torch.cuda.synchronize()
+    assert bitwise_equal(got.cpu().numpy(), expect.cpu().numpy()) == 0
+
+
 @pytest.mark.parametrize("m,n,epi,out_dtype", [(1000, 3000, "gelu", torch.bfloat16), (333, 1536, "none", torch.float32),
                                                (512, 2048, "silu", torch.bfloat16)])
 def test_tile_heights_same_bits(gemm, orc, tile_gemm, m, n, epi, out_dtype):

@@ -91,12 +91,57 @@ def test_block_scaled_reference_entry(gemm, orc):
     judge_blocks(orc, c.cpu().numpy(), x, q, d, block, None, "none", torch.float32)
 
 
+@pytest.mark.parametrize("k", [96, 160, 3072 + 32])
+@pytest.mark.parametrize("layout", ["nk", "kn", "packed"])
+def test_block_scaled_any_k(gemm, orc, k, layout):
+    """Q8_0 with blocks of 32 at K = 32·odd — a valid GGUF shape (the reference computes every 64-row
+    chunk under `row < K`, TensorGEMM.swift:143-171, :162): the activation padded to whole steps with
+    zeros, the packed codes and scales zero past K; against the oracle's fp64 truth of q·d, GELU and
+    SiLU-GLU, bf16 and fp32 out."""
+    m, n, block = 130, 256, 32
+    x, q, d, b = q8_problem(orc, m, k, n, block, 960 + k)
+    for epi in ("none", "gelu", "silu"):
+        glu = epi == "silu"
+        if layout == "nk":
+            w, sc = dev(q).view(torch.int8), dev(d.view(np.int16)).view(torch.float16)
+        else:
+            w, sc = dev(np.ascontiguousarray(q.T)).view(torch.int8), dev(np.ascontiguousarray(d.T).astype(np.float32))
+        if layout == "packed":
+            w, sc = gemm.pack_blocks(w, sc, block, layout="kn", glu=glu), None
+        for out in (torch.bfloat16, torch.float32):
+            y = gemm.product_blocks(bf16_dev(x), w, sc, block, layout="nk" if layout == "nk" else "kn", bias=dev(b),
+                                    epilogue={"none": None, "gelu": "gelu_tanh", "silu": "silu_glu"}[epi],
+                                    out_dtype=out)
+            torch.cuda.synchronize()
+            judge_blocks(orc, y.float().cpu().numpy(), x, q, d, block, b, epi, out)
+
+
+def test_block_scaled_column_slice_kn(gemm, orc):
+    """A column-sliced [K, N] Q8_0 weight (w_full[:, :n]) takes its scales as scale_full[:, :n], rows
+    with the codes' stride: the same bits as the contiguous copy, direct and staged; a contiguous
+    [K/B, n] scale with the wider codes is refused rather than read with the wrong stride."""
+    m, k, n, wide, block = 96, 512, 192, 320, 32
+    x, q, d, b = q8_problem(orc, m, k, wide, block, 77)
+    w_full = dev(np.ascontiguousarray(q.T)).view(torch.int8)               # [K, wide]
+    s_full = dev(np.ascontiguousarray(d.T).astype(np.float32))             # [K/B, wide]
+    w_sl, s_sl = w_full[:, :n], s_full[:, :n]
+    w_c, s_c = w_sl.contiguous(), s_sl.contiguous()
+    a = bf16_dev(x)
+    want = gemm.product_blocks(a, w_c, s_c, block, layout="kn", bias=dev(b[:n]), out_dtype=torch.float32)
+    got = gemm.product_blocks(a, w_sl, s_sl, block, layout="kn", bias=dev(b[:n]), out_dtype=torch.float32)
+    staged = gemm.product_blocks(a, gemm.pack_blocks(w_sl, s_sl, block, layout="kn"), bias=dev(b[:n]),
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(staged, want)
+    judge_blocks(orc, got.cpu().numpy(), x, q[:n], d[:n], block, b[:n], "none", torch.float32)
+    with pytest.raises(ValueError):
+        gemm.product_blocks(a, w_sl, s_c, block, layout="kn")
+    with pytest.raises(ValueError):
+        gemm.pack_blocks(w_sl, s_c, block, layout="kn")
+
+
 def test_block_scaled_refusals(gemm, orc):
     from siliconed_amd import abi
-    x, q, d, b = q8_problem(orc, 8, 96, 64, 32, 3)
-    with pytest.raises(abi.SQ8Error) as e:      # k not a multiple of 64: the activation tiles
-        gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.astype(np.float32)), 32)
-    assert e.value.status == abi.EUNSUPPORTED
     x, q, d, b = q8_problem(orc, 8, 128, 64, 16, 3)
     with pytest.raises(abi.SQ8Error) as e:      # blocks of 16 split an MFMA sub-step
         gemm.product_blocks(bf16_dev(x), dev(q).view(torch.int8), dev(d.astype(np.float32)), 16)
