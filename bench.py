@@ -37,14 +37,24 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
 RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # HBM bytes per launch of the product kernel (FETCH_SIZE × 2 + WRITE_SIZE × 1, the factors from a
-# 512 MiB copy), by (workload, weight layout), as measured by the rocprofv3 --pmc runs recorded in
-# profiles/ (gemm_w256_kernel_c1_up_int8_packed_gelu.md, short_m_skinny_kernel_and_short_tiles.md,
-# hbm_traffic_and_mfma_busy_by_workload.md).
-TRAFFIC_BYTES = {("c1_up", "packed"): 403.6e6, ("c2_skinny", "packed"): 34.89e6, ("c0", "packed"): 56.95e6,
-                 ("skinny_m1", "packed"): 9.70e6, ("skinny_m16", "packed"): 10.53e6, ("skinny_m64", "packed"): 13.19e6,
-                 ("c1_down", "packed"): 450.3e6, ("c2_qkv", "packed"): 415.5e6, ("c3_gate_up", "packed"): 716.4e6,
-                 ("c3_down", "packed"): 367.5e6, ("c3_plain", "packed"): 479.0e6, ("c1_w8a8", "packed"): 472.3e6,
-                 ("c1_q8", "packed"): 592.2e6, ("c1_f32", "packed"): 1007.6e6, ("c1_convrot", "packed"): 403.7e6}
+# 512 MiB copy of the same session), by (workload, weight layout), with the profiles/ summary that records
+# the rocprofv3 --pmc runs they come from; the line reports both, so a kernel change that leaves a figure
+# stale is visible (take the runs again with the commands in that summary).
+TRAFFIC = {("c1_up", "packed"): (403.6e6, "profiles/gemm_w256_kernel_c1_up_int8_packed_gelu.md"),
+           ("c2_skinny", "packed"): (34.89e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
+           ("c0", "packed"): (56.95e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
+           ("skinny_m1", "packed"): (9.70e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
+           ("skinny_m16", "packed"): (10.53e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
+           ("skinny_m64", "packed"): (13.19e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
+           ("c1_down", "packed"): (450.3e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c2_qkv", "packed"): (415.5e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c3_gate_up", "packed"): (716.4e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c3_down", "packed"): (367.5e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c3_plain", "packed"): (479.0e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c1_w8a8", "packed"): (472.3e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c1_q8", "packed"): (592.2e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c1_f32", "packed"): (1007.6e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
+           ("c1_convrot", "packed"): (403.7e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md")}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
 # name: M, K, N, weight type, epilogue, activation distribution, description.
@@ -507,7 +517,8 @@ def main() -> int:
     else:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
-    roofline.update({"traffic": None if args.shape else TRAFFIC_BYTES.get((args.workload, args.layout)),
+    traffic, traffic_src = (None, None) if args.shape else TRAFFIC.get((args.workload, args.layout), (None, None))
+    roofline.update({"traffic": traffic, "traffic_source": traffic_src,
                      "algorithmic_bytes": algo_bytes,
                      "flops": flops, "intensity_flop_per_byte": round(intensity, 1),
                      "hbm_bound_ms": round(algo_bytes / (PEAK_HBM_GBS * 1e9) * 1e3, 5),

@@ -287,8 +287,9 @@ int sq8_linear_quantized(sq8_ctx *ctx, const void *a, int a_dtype, int64_t lda, 
  * forbid hipMalloc). Arguments, arithmetic and results as sq8_linear_quantized (the same kernels, the
  * same bits), but the activation's codes and row scales go to a static scratch array of
  * SQ8_STATIC_SCRATCH_BYTES on each GPU, held from the library's load until the process ends, instead
- * of the context's growable scratch; nothing is allocated or freed and the stream is never
- * synchronized by the call. Limits: the codes (m rows of k rounded up to 128, the total rounded up to
+ * of the context's growable scratch; nothing is allocated or freed and, with `gpu_seconds` NULL, the
+ * stream is never synchronized by the call (a non-NULL `gpu_seconds` records two events and waits for
+ * the second, which graph capture does not allow: pass NULL there). Limits: the codes (m rows of k rounded up to 128, the total rounded up to
  * 256 bytes) and 4·m bytes of row scales must fit (else SQ8_ECAPACITY), and the weight must be
  * packed (SQ8_PACKED / SQ8_PACKED_GLU) or [N, K] int8 with k % 128 == 0, ldw % 16 == 0 and a 16-byte
  * aligned base, the layouts the kernel reads in place (else SQ8_EUNSUPPORTED: a repack would need a
@@ -307,8 +308,8 @@ int64_t sq8_static_scratch_bytes(void);
 /* **A product added into the residual stream**: x[m, n] += gate ⊙ (s ⊙ (A·W) + b), x fp32 (leading
  * dimension ldx) read and written in place, gate fp32 [n] or NULL (1), the sum in fp32 (not rounded
  * to bf16 first), then x + gate·y with each product and sum rounded on its own. Arguments otherwise
- * as sq8_linear (no activation); weights packed or [N, K] with K a multiple of 64 (else
- * SQ8_EUNSUPPORTED). Replaces: the Wo / W_down product and `x += gate · …` of a DiT block
+ * as sq8_linear (no activation); any K (a K that is not a multiple of 64 is padded with zeros in the
+ * context's scratch, the weight repacked per product). Replaces: the Wo / W_down product and `x += gate · …` of a DiT block
  * (MossImage.swift:15-19; the residual loop of ElementwiseGPUAnima.swift:47-62), one pass. */
 int sq8_linear_residual(sq8_ctx *ctx,
                         const void *a, int a_dtype, int64_t lda,

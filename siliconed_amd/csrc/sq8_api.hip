@@ -36,6 +36,7 @@ struct sq8_ctx {
     int wd_tile;            // measurement knobs, read once at sq8_create (SQ8_TILE, SQ8_Q8_TILE, SQ8_SPLITS): a
     int q8_tile;            // forced weight-direct / block-scale tile, or -1 (the product's own choice); the
     int splits;             // skinny kernel's K split count (1: none, the default)
+    int cus;                // the device's compute units, read once here: the tile rules' rounds
 };
 
 namespace {
@@ -352,7 +353,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
-        const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue));
+        const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue), ctx->cus);
         if ((tile == sq8::WD_SKINNY32 || tile == sq8::WD_SKINNY64) && ctx->splits > 1) {
             // Short M with the SQ8_SPLITS knob: the K steps split over several workgroups per tile, partial
             // sums in the context's buffer, added in split order by a second launch. Not the default: the
@@ -373,7 +374,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         return SQ8_EUNSUPPORTED;  // the residual epilogue and the fp32 route run on the weight-direct kernels only
     } else {
         const int wl = q.w_layout == SQ8_KN ? sq8::W_KN : sq8::W_NK;
-        const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue));
+        const int tile = sq8::choose_tile(q.m, n_out, is_glu(q.epilogue), ctx->cus);
         const bool fast = p.a_vec && p.w_vec && k_steps && cols_per_half >= 4 &&
                           (q.w_layout == SQ8_NK || (cols_per_half % 4) == 0);
         e = sq8::launch_gemm(p, fast, tile, wt, wl, q.epilogue, out, ctx->stream);
@@ -774,8 +775,10 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
     memset(ctx, 0, sizeof(*ctx));
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);
+    ctx->cus = prop.multiProcessorCount;
     ctx->wd_tile = knob(getenv("SQ8_TILE"), {{"256", sq8::WD_256}, {"224", sq8::WD_224}, {"128", sq8::WD_128}, {"64", sq8::WD_64},
-                                             {"32", sq8::WD_32}, {"64n", sq8::WD_64N}, {"64x192", sq8::WD_64x192}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32}});
+                                             {"32", sq8::WD_32}, {"64n", sq8::WD_64N}, {"64x192", sq8::WD_64x192}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32},
+                                             {"gemv", sq8::WD_GEMV}});
     ctx->q8_tile = knob(getenv("SQ8_Q8_TILE"), {{"256", sq8::BL_64x256}, {"512", sq8::BL_64x512},
                                                 {"128x256", sq8::BL_128x256}, {"128x128", sq8::BL_128x128}});
     const char *splits = getenv("SQ8_SPLITS");

@@ -108,10 +108,10 @@ __device__ __forceinline__ float tanh_fast(float y) {
 // x/∞ = −0 for large negative x, as the tanh form's ½·x·0. The exponent −2u·log2(e) is
 // x·(k + k·0.044715·x²), k = −2·√(2/π)·log2(e), its constant folded into the polynomial (seven
 // vector instructions a value).
+constexpr float kGeluK = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634);
+constexpr float kGeluK3 = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634 * 0.044715);
 __device__ __forceinline__ float gelu_tanh(float x) {
-    constexpr float k = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634);
-    constexpr float k3 = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634 * 0.044715);
-    const float t = __builtin_fmaf(k3, x * x, k);
+    const float t = __builtin_fmaf(kGeluK3, x * x, kGeluK);
     const float e = __builtin_amdgcn_exp2f(x * t);
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }

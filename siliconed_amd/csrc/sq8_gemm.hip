@@ -19,39 +19,43 @@ hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, 
     return wl == W_NK ? launch_wdirect_1_1(p, tile, epi, out, stream) : launch_wdirect_1_2(p, tile, epi, out, stream);
 }
 
-int choose_wd_tile(int M, int N, bool glu) {
+int choose_wd_tile(int M, int N, bool glu, int cus) {
     // Tiles of 256 columns (four 64-column slabs; GLU: 32 output columns a slab), as tall as keeps
-    // at least 144 of them — the measured point below which a shorter tile fills the 256 CUs better
-    // than the taller one loses (K = 3072: M = 1024 at N = 3072 runs 64-row tiles at one workgroup a
-    // CU in 28.5 µs against 42.8 in 128-row tiles; M = 512 32-row tiles in 22.7 against 42.9). Below
-    // 144 tiles of 32 rows, the skinny kernel (K split over four waves): 32-row tiles to M = 128,
-    // 64-row above (M = 16: 8.3 µs against 20.2 for 32-row tiles of the main kernel).
+    // at least 9/16 of the CUs' worth of them (144 on the 256 CUs of a whole MI355X) — the measured point
+    // below which a shorter tile fills the CUs better than the taller one loses (K = 3072: M = 1024 at
+    // N = 3072 runs 64-row tiles at one workgroup a CU in 28.5 µs against 42.8 in 128-row tiles; M = 512
+    // 32-row tiles in 22.7 against 42.9). Below that in 32-row tiles, the skinny kernel (K split over four
+    // waves): 32-row tiles to M = 128, 64-row above (M = 16: 8.3 µs against 20.2 for 32-row tiles of the
+    // main kernel). `cus`: the device's compute units (a compute-partitioned MI355X has fewer than 256),
+    // so a round is `cus` tiles of one workgroup a CU.
+    if (cus <= 0) cus = 256;
     const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
     const long tn = (slabs + 3) / 4;
+    const long fill = (long)cus * 9 / 16;
     auto tiles = [&](int bm) { return (long)((M + bm - 1) / bm) * tn; };
-    // 256 × 256 tiles (one workgroup a CU) once they occupy more than half the 256 CUs: C1's
+    // 256 × 256 tiles (one workgroup a CU) once they occupy more than half the CUs: C1's
     // up-projection, 768 tiles, 243.6 µs against 265.1 in 128-row tiles (one process, medians); C3's fp8
     // gate-up (SiLU-GLU, 1280 tiles) 1353 against 1290 TFLOP/s; C1's down-projection, 192 tiles (one
     // partial round), 1208–1228 against 1105. With fewer, the 128-row tiles spread over more CUs.
-    if (tiles(256) > 128) {
-        // 224-row tiles where their rounds on the 256 CUs cover fewer rows than the 256-row tiles' (the
+    if (tiles(256) > cus / 2) {
+        // 224-row tiles where their rounds on the CUs cover fewer rows than the 256-row tiles' (the
         // same work per row, one workgroup a CU): C1's down-projection (M = 4096, N = 3072) 228 tiles in
         // one round against 192 in one; C4's and C2's fused QKV (M = 4608, N = 9216) 756 tiles in three
         // rounds against 648 in three; never C1's up-projection (768 tiles, three full rounds).
-        auto rows = [&](int bm) { return (tiles(bm) + 255) / 256 * bm; };
+        auto rows = [&](int bm) { return (tiles(bm) + cus - 1) / cus * bm; };
         return rows(224) < rows(256) ? WD_224 : WD_256;
     }
-    if (tiles(128) >= 144) return WD_128;
-    if (tiles(64) >= 144) {
-        // 64 × 192 tiles of six one-block waves while they fit one round on the 256 CUs (and not for the GLU
+    if (tiles(128) >= fill) return WD_128;
+    if (tiles(64) >= fill) {
+        // 64 × 192 tiles of six one-block waves while they fit one round on the CUs (and not for the GLU
         // epilogues): less activation and weight per workgroup for the same rows. Measured against the 64-row
         // tiles at K = 3072 in one process: C0 (1024 × 3072) 29.7 against 30.9 µs, and 3–5 % faster on five
         // other shapes of one round (768 × 3072, 192 and 256 × 12288, 256 × 9216); past one round (1280 × 3072,
         // 384 × 9216) 1.6× slower, so not there.
         const long tiles64x192 = (long)((M + 63) / 64) * ((N + 191) / 192);
-        return !glu && tiles64x192 <= 256 ? WD_64x192 : WD_64;
+        return !glu && tiles64x192 <= cus ? WD_64x192 : WD_64;
     }
-    if (tiles(32) >= 144) {
+    if (tiles(32) >= fill) {
         // 64 × 128 tiles, a 32-column block a wave (half the codes widened per MFMA), where they add no tiles
         // to the 32-row ones (a ragged last row tile would): measured over 15 shapes at K = 3072 in one
         // process, C2's text stream (512 × 3072) 20.5 against 23.3 µs, the shapes whose 32-row tiles number
@@ -69,11 +73,12 @@ int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits) {
     return (int64_t)splits * tiles * (2 * (bm / 32)) * 1024 * 4;
 }
 
-int choose_tile(int M, int N_out, bool glu) {
-    // Tiles of 256 × 256 while they fill the 256 CUs at least 3/4 of the way; 128 × 128 below.
+int choose_tile(int M, int N_out, bool glu, int cus) {
+    // Tiles of 256 × 256 while they fill the CUs at least 3/4 of the way; 128 × 128 below.
+    if (cus <= 0) cus = 256;
     const int n_virtual = glu ? 2 * N_out : N_out;
     const long big = (long)((M + 255) / 256) * ((n_virtual + 255) / 256);
-    return big >= 192 ? TILE_256x256 : TILE_128x128;
+    return big >= (long)cus * 3 / 4 ? TILE_256x256 : TILE_128x128;
 }
 
 hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, int epi, int out, hipStream_t stream) {

@@ -1,5 +1,6 @@
 // sq8_wdirect_inst.hip — instantiates the weight-direct kernels for one weight type (SQ8_WT) and
 // layout (SQ8_WL: 1 [N, K], 2 packed), compiled once per pair so the sets build in parallel.
+#include "sq8_gemv_kernel.h"
 #include "sq8_skinny_kernel.h"
 #include "sq8_w256_kernel.h"
 
@@ -37,6 +38,13 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
         tile = WD_32;
     }
     if (tile == WD_32) return wd::dispatch_wd<32, 4, 2, SQ8_WT, SQ8_WL, 4>(p, epi, out, stream);
+    if (tile == WD_GEMV) {
+        // 16 rows a group of MFMAs; eight K steps of loads in flight (four for 64 rows: the registers).
+        if (p.M <= 16) return wd::dispatch_gemv<1, 8, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+        if (p.M <= 32) return wd::dispatch_gemv<2, 6, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+        if (p.M <= 64) return wd::dispatch_gemv<4, 4, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+        tile = WD_SKINNY64;
+    }
     if (tile == WD_SKINNY64) return wd::dispatch_skinny<64, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_SKINNY32) return wd::dispatch_skinny<32, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     return hipErrorInvalidValue;

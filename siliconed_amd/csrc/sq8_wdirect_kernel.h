@@ -238,38 +238,87 @@ __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_
 }
 
 
+// Scale, bias and activation of the 16 values of one accumulator block (a lane's columns 8g + 4h + e,
+// value 4g + e), GLU: with the 16 of the paired block `u` (scales and biases `cu`). Each operation is
+// applied to all 16 values before the next one, so a single wave per SIMD issues 16 independent
+// instructions back to back instead of stalling on each value's dependent chain (GELU's is seven
+// instructions with two transcendental ones); the operations per value are exactly those of gelu_tanh,
+// silu_glu and situ (sq8_device.h), after __fmul_rn by the scale and __fadd_rn of the bias.
+template <int EPI, bool HB>
+__device__ __forceinline__ void block_values(const f32x16 &x, const ColParams &cx, const f32x16 &u, const ColParams &cu,
+                                             float (&v)[16]) {
+    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
+    float t[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = __fmul_rn(x[e], cx.s[e >> 2][e & 3]);
+    if constexpr (HB) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = __fadd_rn(v[e], cx.b[e >> 2][e & 3]);
+    }
+    if constexpr (EPI == EPI_GELU) {
+        // gelu_tanh: x / (1 + 2^(x·(k + k3·x²))).
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = v[e] * v[e];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = __builtin_fmaf(kGeluK3, t[e], kGeluK);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = v[e] * t[e];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = __builtin_amdgcn_exp2f(t[e]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = 1.0f + t[e];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = __builtin_amdgcn_rcpf(t[e]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] * t[e];
+    } else if constexpr (GLU) {
+        float w[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) w[e] = __fmul_rn(u[e], cu.s[e >> 2][e & 3]);
+        if constexpr (HB) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) w[e] = __fadd_rn(w[e], cu.b[e >> 2][e & 3]);
+        }
+        if constexpr (EPI == EPI_SILU_GLU) {
+            // silu_glu: g · 1/(1 + 2^(−g·log2 e)) · u.
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[e] = v[e] * -1.4426950408889634f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[e] = __builtin_amdgcn_exp2f(t[e]);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[e] = 1.0f + t[e];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[e] = __builtin_amdgcn_rcpf(t[e]);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = v[e] * t[e];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = v[e] * w[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = situ(v[e], w[e]);
+        }
+    }
+}
+
 // Scale, bias and activation of one 32 × 32 output block (GLU: the pair of blocks) a wave holds in
 // `x` (and `u`, with `cu`), written to the wave's LDS region as rows of 32 values, then stored as
 // 16-byte row segments. Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
 template <int EPI, int OUT, bool HB>
 __device__ __forceinline__ void stage_block(const f32x16 &x, const ColParams &cx, const f32x16 &u, const ColParams &cu,
                                             uint8_t *region, int lane) {
-    constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
     constexpr int PITCH = 32 * ESZ + 16;  // row bytes + 16: keeps 16-byte alignment, spreads banks
     const int h = lane >> 5, r = lane & 31;
+    float y[16];
+    block_values<EPI, HB>(x, cx, u, cu, y);
     static_for<0, 4>([&](auto gc) {
         constexpr int g = decltype(gc)::value;
         const int c = 8 * g + 4 * h;  // first of this lane's 4 columns in the block
-        float y[4];
-        static_for<0, 4>([&](auto ec) {
-            constexpr int e = decltype(ec)::value;
-            float v = __fmul_rn(x[4 * g + e], cx.s[g][e]);
-            if constexpr (HB) v = __fadd_rn(v, cx.b[g][e]);
-            if constexpr (EPI == EPI_GELU) {
-                v = gelu_tanh(v);
-            } else if constexpr (GLU) {
-                float w = __fmul_rn(u[4 * g + e], cu.s[g][e]);
-                if constexpr (HB) w = __fadd_rn(w, cu.b[g][e]);
-                v = EPI == EPI_SILU_GLU ? silu_glu(v, w) : situ(v, w);
-            }
-            y[e] = v;
-        });
         uint8_t *dst = region + r * PITCH + c * ESZ;
         if constexpr (OUT == OUT_BF16)
-            *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16_rne(y[4 * g], y[4 * g + 1]), pack_bf16_rne(y[4 * g + 2], y[4 * g + 3])};
         else
-            *reinterpret_cast<f32x4 *>(dst) = f32x4{y[0], y[1], y[2], y[3]};
+            *reinterpret_cast<f32x4 *>(dst) = f32x4{y[4 * g], y[4 * g + 1], y[4 * g + 2], y[4 * g + 3]};
     });
 }
 
@@ -285,47 +334,52 @@ __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, 
     flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
 }
 
+// The 16 values of one accumulator block as 8 bf16 pairs (block_values, then nearest-even pairs).
+template <int EPI, bool HB>
+__device__ __forceinline__ void block_bf16_pairs(const f32x16 &a, const ColParams &c, uint32_t (&pk)[8]) {
+    float v[16];
+    block_values<EPI, HB>(a, c, a, c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pk[i] = pack_bf16_rne(v[2 * i], v[2 * i + 1]);
+}
+
 // The bf16 epilogue of one whole 64-column slab (columns [col0, col0 + 64) of the product, in one
-// output and one head): scale, bias and activation in registers; the wave's 32·FM × 64 outputs are
-// written to its LDS region (rows of 128 bytes, 16-byte chunks XOR-swizzled by row & 7) and read
-// back as 16-byte chunks, eight lanes a row, so each store instruction writes eight whole 128-byte
-// row segments. No wait between the blocks: all values are staged, then all are stored. Rows past M
-// are not stored. `region`: 32·FM·128 bytes of the wave's own.
+// output and one head), 32 rows at a time: both 32-column blocks of a row block are scaled, biased and
+// activated in registers (block_bf16_pairs), written to the wave's LDS region (rows of 128 bytes, 16-byte
+// chunks XOR-swizzled by row & 7) and read back as 16-byte chunks, eight lanes a row, so each store
+// instruction writes eight whole 128-byte row segments; the row block's stores are in flight while the
+// next one is computed. Rows past M are not stored. `region`: 32·FM·128 bytes of the wave's own.
 template <int FM, int EPI, bool HB>
-__device__ __forceinline__ void stage_slab_bf16(const f32x16 (&acc)[2][FM], const ColParams (&cp)[2], uint8_t *region,
-                                                int lane) {
-    const int h = lane >> 5, r = lane & 31;
+__device__ __forceinline__ void slab_rows_bf16(const GemmArgs &p, const f32x16 (&acc)[2][FM], const ColParams (&cp)[2],
+                                               int m0, uint8_t *out, int64_t pitch, uint8_t *region, int lane) {
+    const int h = lane >> 5, r = lane & 31, chunk = lane & 7;
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
+        __builtin_amdgcn_sched_barrier(0);
         static_for<0, 2>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
+            uint32_t pk[8];
+            block_bf16_pairs<EPI, HB>(acc[b][bm], cp[b], pk);
+            const int row = 32 * bm + r;
             static_for<0, 4>([&](auto gc) {
                 constexpr int g = decltype(gc)::value;
-                float y[4];
-                static_for<0, 4>([&](auto ec) {
-                    constexpr int e = decltype(ec)::value;
-                    float v = __fmul_rn(acc[b][bm][4 * g + e], cp[b].s[g][e]);
-                    if constexpr (HB) v = __fadd_rn(v, cp[b].b[g][e]);
-                    if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
-                    y[e] = v;
-                });
-                const int row = 32 * bm + r;
-                const int chunk = 4 * b + g;  // 8 columns: 8g + [0, 8) of block b; this lane's half h
-                *reinterpret_cast<u32x2 *>(region + row * 128 + ((chunk ^ (row & 7)) << 4) + 8 * h) =
-                    u32x2{pack_bf16_rne(y[0], y[1]), pack_bf16_rne(y[2], y[3])};
+                const int ch = 4 * b + g;  // 8 columns: 8g + [0, 8) of block b; this lane's half h
+                *reinterpret_cast<u32x2 *>(region + row * 128 + ((ch ^ (row & 7)) << 4) + 8 * h) =
+                    u32x2{pk[2 * g], pk[2 * g + 1]};
             });
+        });
+        static_for<0, 4>([&](auto ic) {
+            constexpr int i = 4 * bm + decltype(ic)::value;
+            const int row = 8 * i + (lane >> 3);
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(region + row * 128 + ((chunk ^ (row & 7)) << 4));
+            if (m0 + row < p.M) *reinterpret_cast<u32x4 *>(out + (int64_t)row * pitch * 2) = v;
         });
     });
 }
 
-// (The bias test is one uniform branch around the whole slab, not a select per value.)
 template <int FM, int EPI>
 __device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x16 (&acc)[2][FM], const ColParams (&cp)[2],
                                                    bool has_bias, int m0, int col0, uint8_t *region, int lane) {
-    if (has_bias)
-        stage_slab_bf16<FM, EPI, true>(acc, cp, region, lane);
-    else
-        stage_slab_bf16<FM, EPI, false>(acc, cp, region, lane);
     // Where the slab's rows go: output `which` of the QKV split, then row-major (ldc) or head-major
     // ([heads, M, head_dim]: consecutive rows of one head are head_dim apart).
     int which = 0, cc = col0;
@@ -342,14 +396,12 @@ __device__ __forceinline__ void slab_epilogue_bf16(const GemmArgs &p, const f32x
         first = (int64_t)m0 * p.ldc + cc;
         pitch = p.ldc;
     }
-    const int chunk = lane & 7;
-    uint8_t *const out = kern::out_base(p, which) + (first + chunk * 8) * 2;
-    static_for<0, 4 * FM>([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
-        const int row = 8 * i + (lane >> 3);
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(region + row * 128 + ((chunk ^ (row & 7)) << 4));
-        if (m0 + row < p.M) *reinterpret_cast<u32x4 *>(out + (int64_t)row * pitch * 2) = v;
-    });
+    uint8_t *const out = kern::out_base(p, which) + (first + (lane & 7) * 8) * 2;
+    // (The bias test is one uniform branch around the whole slab, not a select per value.)
+    if (has_bias)
+        slab_rows_bf16<FM, EPI, true>(p, acc, cp, m0, out, pitch, region, lane);
+    else
+        slab_rows_bf16<FM, EPI, false>(p, acc, cp, m0, out, pitch, region, lane);
 }
 
 // True when a kernel's slab epilogue serves this product: bf16 output, a plain or GELU epilogue,

@@ -53,6 +53,12 @@ def test_hostile_headers(tmp_path):
     refused(gguf(tmp_path, "array.gguf", 1, gstr("a") + le("I", 9) + le("I", 10) + le("Q", 30)), "cannot fit")
     refused(gguf(tmp_path, "align.gguf", 1, gstr("general.alignment") + le("I", 10) + le("Q", 1 << 62)),
             "general.alignment")
+    # A string-typed alignment is read as the reference's Int(a): an optional sign and ASCII digits.
+    for i, text in enumerate(["²", "٣٢", "3 2", ""]):
+        refused(gguf(tmp_path, f"salign{i}.gguf", 1, gstr("general.alignment") + le("I", 8) + gstr(text)),
+                "general.alignment")
+    with GGUFFile(gguf(tmp_path, "plus.gguf", 1, gstr("general.alignment") + le("I", 8) + gstr("+64"))) as f:
+        assert f.header.alignment == 64
     info = gstr("w") + le("I", 4) + b"".join(le("Q", 69_000) for _ in range(4)) + le("I", 0) + le("Q", 0)
     refused(gguf(tmp_path, "dims.gguf", 0, b"", 1, info, size=70_000), "overflow a 64-bit count")
     # A header read in part: Unread past the bytes read, never a verdict on zeros; whole, it parses.

@@ -289,6 +289,52 @@ def test_baseline_shapes_sampled_rows(gemm, orc, case):
         judge(orc, got, x, q, fp8, s, b, epi, torch.bfloat16, rows=orc.sample_rows(m, 64))
 
 
+@pytest.mark.parametrize("head_dim", [0, 128])
+def test_fused_qkv_c2_full_shape(gemm, orc, head_dim):
+    """configs[2]'s fused QKV at its full shape (X [4608, 3072], W [9216, 3072] int8, packed as staged):
+    Q, K and V row-major or head-major ([24 heads, 4608, 128], MossImage.swift:548-560), judged against
+    the oracle's fp64 truth on 64 sampled rows across all 9216 columns."""
+    m, k, d = 4608, 3072, 3072
+    print(f"fused qkv {m}x{k}x{3 * d} head_dim {head_dim}", flush=True)
+    x, q, s, b = problem(orc, m, k, 3 * d, False, 2200 + head_dim)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    qq, kk, vv = gemm.product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(m, 64)
+    ridx = torch.from_numpy(rows.astype(np.int64)).to(DEV)
+    parts = []
+    for t in (qq, kk, vv):
+        t = t.index_select(1, ridx).permute(1, 0, 2).reshape(len(rows), d) if head_dim else t.index_select(0, ridx)
+        parts.append(t.float().cpu().numpy())
+    judge(orc, np.concatenate(parts, axis=1), x[rows], q, False, s, b, "none", torch.bfloat16,
+          rows=np.arange(len(rows)))
+
+
+def test_c1_down_on_up_gelu_output(gemm, orc):
+    """configs[1] as chained: the up projection (X [4096, 3072] ~ N(0, 1), W_up [12288, 3072], bias, GELU)
+    and the down projection (W_down [3072, 12288], bias) on the up projection's bf16 output — many
+    near-zero activations, not N(0, 1). Each product judged against the oracle on 64 sampled rows, the
+    down projection on the very activation the GPU produced."""
+    m, k, n = 4096, 3072, 12288
+    x, q_up, s_up, b_up = problem(orc, m, k, n, False, 2300)
+    _, q_dn, s_dn, b_dn = problem(orc, 8, n, k, False, 2400)
+    w_up = gemm.pack(weight_tensor(q_up, False, "nk"), layout="nk")
+    w_dn = gemm.pack(weight_tensor(q_dn, False, "nk"), layout="nk")
+    h = gemm.product(bf16_dev(x), w_up, dev(s_up), bias=dev(b_up), epilogue="gelu_tanh")
+    y = gemm.product(h, w_dn, dev(s_dn), bias=dev(b_dn))
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(m, 64)
+    ridx = torch.from_numpy(rows.astype(np.int64)).to(DEV)
+    sub = np.arange(len(rows))
+    h_rows = h.index_select(0, ridx)
+    h_bits = h_rows.view(torch.int16).cpu().numpy().view(np.uint16)
+    judge(orc, h_rows.float().cpu().numpy(), x[rows], q_up, False, s_up, b_up, "gelu", torch.bfloat16, rows=sub)
+    near_zero = float((np.abs(orc.bf16_to_f32(h_bits)) < 1e-2).mean())
+    assert near_zero > 0.05, near_zero   # the GELU output's distribution, not N(0, 1)
+    judge(orc, y.index_select(0, ridx).float().cpu().numpy(), h_bits, q_dn, False, s_dn, b_dn, "none", torch.bfloat16,
+          rows=sub)
+
+
 # ---- the packed layout (sq8_pack_weight) ------------------------------------------------------------
 
 PACKED_SHAPES = [(256, 3072, 3072), (150, 768, 96), (70, 10240, 72), (65, 448, 130), (300, 1024, 1000), (1, 64, 8)]

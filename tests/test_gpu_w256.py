@@ -32,6 +32,12 @@ def product(tile_gemm, tile, x, w, s, b, layout, epi, out_dtype=torch.bfloat16):
     (777, 768, 640, True, "packed", "none", True, False),       # fp8, ragged rows, 2 + 2 + 2... slabs
     (256, 2048, 768, True, "nk", "gelu", True, True),           # fp8 in place, one scale for the tensor
     (1, 512, 512, False, "packed", "gelu", True, False),        # one row
+    # K steps not a multiple of four (the loop's leftover steps: 5, 7 and 9 steps leave 1, 3 and 1; 6 leaves
+    # 2), at full row tiles and several column tiles, for both tile heights.
+    (768, 320, 1024, False, "packed", "gelu", True, False),
+    (600, 448, 1280, False, "nk", "none", True, False),
+    (1024, 576, 768, True, "packed", "gelu", True, False),
+    (512, 384, 1024, False, "packed", "none", True, False),
 ])
 def test_w256_same_bits_as_128(gemm, orc, tile_gemm, m, k, n, fp8, layout, epi, bias, tensor_scale):
     x, q, s, b = problem(orc, m, k, n, fp8, 400 + m + n, bias=bias)

@@ -15,28 +15,33 @@ DEV = "cuda:0"
 
 
 def _static(gemm, x, w, s, b, group, epi, out):
+    """`w`: a PackedWeight, or [N, K] int8 codes read in place (layout NK, ldw = its row stride)."""
     m, k = x.shape
-    secs = ctypes.c_double(0.0)
+    if isinstance(w, torch.Tensor):
+        wptr, lay, ldw, n = w.data_ptr(), abi.NK, w.stride(0), w.shape[0]
+    else:
+        wptr, lay, ldw, n = w.data.data_ptr(), w.layout, w.k, w.n
     st = abi.load().sq8_linear_quantized_static(
         gemm._h, x.data_ptr(), abi.F32 if x.dtype == torch.float32 else abi.BF16, x.stride(0), group,
-        w.data.data_ptr(), w.layout, w.k, s.data_ptr(), abi.SCALE_COLUMNS, None if b is None else b.data_ptr(), epi,
-        out.data_ptr(), abi.BF16 if out.dtype == torch.bfloat16 else abi.F32, out.stride(0), m, k, w.n,
-        ctypes.byref(secs))
+        wptr, lay, ldw, s.data_ptr(), abi.SCALE_COLUMNS, None if b is None else b.data_ptr(), epi,
+        out.data_ptr(), abi.BF16 if out.dtype == torch.bfloat16 else abi.F32, out.stride(0), m, k, n, None)
     return st
 
 
+@pytest.mark.parametrize("layout", ["packed", "nk"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
-def test_static_scratch_equals_the_allocating_route(gemm, orc, out_dtype):
+def test_static_scratch_equals_the_allocating_route(gemm, orc, out_dtype, layout):
+    """Packed weights, and [N, K] codes read in place (k % 128 == 0, 16-byte aligned rows)."""
     cases = [(2048, 3072, 3072, 256, abi.EPI_GELU_TANH, "gelu_tanh"),   # 6.3 MB of codes
              (37, 1024, 640, 0, abi.EPI_NONE, None)]                     # smaller: the first call's codes remain
     for i, (m, k, n, group, epi, name) in enumerate(cases):
-        print(f"static scratch call {i}: m {m} k {k} n {n} group {group} out {out_dtype}", flush=True)
+        print(f"static scratch call {i}: {layout} m {m} k {k} n {n} group {group} out {out_dtype}", flush=True)
         x = torch.from_numpy(orc.normal_f32(40 + i, (m, k))).to(DEV)
         q = torch.from_numpy(orc.uniform_i8(41 + i, (n, k))).to(DEV)
         s = torch.from_numpy(orc.uniform_f32(42 + i, (n,), 1e-3, 2e-2)).to(DEV)
         b = torch.from_numpy(orc.normal_f32(43 + i, (n,), 0.0, 0.02)).to(DEV)
-        w = gemm.pack(q, layout="nk")
-        want = gemm.product_quantized(x, w, s, group=group, bias=b, epilogue=name, out_dtype=out_dtype)
+        w = gemm.pack(q, layout="nk") if layout == "packed" else q
+        want = gemm.product_quantized(x, w, s, layout="nk", group=group, bias=b, epilogue=name, out_dtype=out_dtype)
         got = torch.full((m, n), float("nan"), dtype=out_dtype, device=DEV)
         assert _static(gemm, x, w, s, b, group, epi, got) == abi.OK
         torch.cuda.synchronize()
