@@ -329,6 +329,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         p.kt_w = p.kt;  // the weight's steps; the activation has three parts of them
         p.kt = 3 * p.kt_w;
     }
+    p.cus = ctx->cus;
     hipError_t e;
     // [K, N] codes in place: repacked per product into the context's buffer when the repack runs near
     // the memory bandwidth (the reference's in-place route, Artifact.swift:443-459, at the speed of

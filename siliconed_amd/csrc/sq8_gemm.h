@@ -36,6 +36,7 @@ struct GemmArgs {
     float *part;            // the skinny kernel's K split: fp32 partial sums, skinny_part_bytes() of them
     int splits;             // > 1: the skinny kernel's K steps split over this many workgroups per tile, whose
                             // sums a second launch adds in split order before the epilogue
+    int cus;                // the device's compute units (0: 256), for launch shapes chosen per product
 };
 
 enum Tile { TILE_256x256 = 0, TILE_128x128 = 1 };

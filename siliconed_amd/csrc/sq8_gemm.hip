@@ -26,7 +26,7 @@ int choose_wd_tile(int M, int N, bool glu, int cus) {
     // N = 3072 runs 64-row tiles at one workgroup a CU in 28.5 µs against 42.8 in 128-row tiles; M = 512
     // 32-row tiles in 22.7 against 42.9). Below that in 32-row tiles, the skinny kernel (K split over four
     // waves): 32-row tiles to M = 128, 64-row above (M = 16: 8.3 µs against 20.2 for 32-row tiles of the
-    // main kernel). `cus`: the device's compute units (a compute-partitioned MI355X has fewer than 256),
+    // main kernel); up to 16 rows on narrow weights, the short-M kernel. `cus`: the device's compute units (a compute-partitioned MI355X has fewer than 256),
     // so a round is `cus` tiles of one workgroup a CU.
     if (cus <= 0) cus = 256;
     const long slabs = glu ? (N / 2 + 31) / 32 : (N + 63) / 64;
@@ -64,6 +64,13 @@ int choose_wd_tile(int M, int N, bool glu, int cus) {
         const long tiles64n = (long)((M + 63) / 64) * ((N + 127) / 128);
         return !glu && tiles64n <= tiles(32) ? WD_64N : WD_32;
     }
+    // Up to 16 rows, the 16-column groups of the short-M kernel where they fit one round on the CUs (N ≤ 4096
+    // on 256 CUs; GLU: 2048 output columns): every K step's loads in flight, the activation read once per
+    // workgroup. Kernel traces at K = 3072, N = 3072 (int8 packed, bias): M = 1 4.10 µs against the skinny
+    // kernel's 7.44, M = 16 5.95 against 8.73; K = 12288, N = 3072: M = 1 10.1 against 19.4. Past one round
+    // (N = 9216, 12288) the skinny kernel's 64-column slabs stream better (M = 8: 8.3 against 11.6 µs).
+    const long gemv_groups = glu ? (N / 2 + 7) / 8 : (N + 15) / 16;
+    if (M <= 16 && gemv_groups <= cus) return WD_GEMV;
     return M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
 }
 

@@ -39,11 +39,9 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
     }
     if (tile == WD_32) return wd::dispatch_wd<32, 4, 2, SQ8_WT, SQ8_WL, 4>(p, epi, out, stream);
     if (tile == WD_GEMV) {
-        // 16 rows a group of MFMAs; eight K steps of loads in flight (four for 64 rows: the registers).
-        if (p.M <= 16) return wd::dispatch_gemv<1, 8, SQ8_WT, SQ8_WL>(p, epi, out, stream);
-        if (p.M <= 32) return wd::dispatch_gemv<2, 6, SQ8_WT, SQ8_WL>(p, epi, out, stream);
-        if (p.M <= 64) return wd::dispatch_gemv<4, 4, SQ8_WT, SQ8_WL>(p, epi, out, stream);
-        tile = WD_SKINNY64;
+        // Up to 16 rows (one group of 16 × 16 MFMAs); more rows take the skinny kernel.
+        if (p.M <= 16) return wd::dispatch_gemv<SQ8_WT, SQ8_WL>(p, epi, out, stream);
+        tile = p.M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
     }
     if (tile == WD_SKINNY64) return wd::dispatch_skinny<64, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
     if (tile == WD_SKINNY32) return wd::dispatch_skinny<32, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
