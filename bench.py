@@ -40,21 +40,23 @@ RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 # 512 MiB copy of the same session), by (workload, weight layout), with the profiles/ summary that records
 # the rocprofv3 --pmc runs they come from; the line reports both, so a kernel change that leaves a figure
 # stale is visible (take the runs again with the commands in that summary).
-TRAFFIC = {("c1_up", "packed"): (403.6e6, "profiles/gemm_w256_kernel_c1_up_int8_packed_gelu.md"),
-           ("c2_skinny", "packed"): (34.89e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
-           ("c0", "packed"): (56.95e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
-           ("skinny_m1", "packed"): (9.70e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
-           ("skinny_m16", "packed"): (10.53e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
-           ("skinny_m64", "packed"): (13.19e6, "profiles/short_m_skinny_kernel_and_short_tiles.md"),
-           ("c1_down", "packed"): (450.3e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c2_qkv", "packed"): (415.5e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c3_gate_up", "packed"): (716.4e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c3_down", "packed"): (367.5e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c3_plain", "packed"): (479.0e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c1_w8a8", "packed"): (472.3e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c1_q8", "packed"): (592.2e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c1_f32", "packed"): (1007.6e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md"),
-           ("c1_convrot", "packed"): (403.7e6, "profiles/hbm_traffic_and_mfma_busy_by_workload.md")}
+_TRAFFIC_SRC = "profiles/hbm_traffic_by_workload.md"
+TRAFFIC = {
+    ("c1_up", "packed"): (403.6e6, _TRAFFIC_SRC),
+    ("c2_skinny", "packed"): (34.91e6, _TRAFFIC_SRC),
+    ("c0", "packed"): (56.98e6, _TRAFFIC_SRC),
+    ("skinny_m1", "packed"): (9.68e6, _TRAFFIC_SRC),
+    ("skinny_m16", "packed"): (10.52e6, _TRAFFIC_SRC),
+    ("skinny_m64", "packed"): (13.18e6, _TRAFFIC_SRC),
+    ("c1_down", "packed"): (450.35e6, _TRAFFIC_SRC),
+    ("c2_qkv", "packed"): (415.51e6, _TRAFFIC_SRC),
+    ("c3_gate_up", "packed"): (715.93e6, _TRAFFIC_SRC),
+    ("c3_down", "packed"): (367.51e6, _TRAFFIC_SRC),
+    ("c3_plain", "packed"): (478.92e6, _TRAFFIC_SRC),
+    ("c1_w8a8", "packed"): (472.42e6, _TRAFFIC_SRC),
+    ("c1_q8", "packed"): (592.23e6, _TRAFFIC_SRC),
+    ("c1_f32", "packed"): (1007.54e6, _TRAFFIC_SRC),
+    ("c1_convrot", "packed"): (403.59e6, _TRAFFIC_SRC)}
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
 
 # name: M, K, N, weight type, epilogue, activation distribution, description.

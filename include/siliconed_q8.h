@@ -141,7 +141,8 @@ int sq8_linear(sq8_ctx *ctx,
  * 296-360), judged by its fp32 bar (≤ 1e-5 per channel, Diagnostic.swift:105). Each value is split into three
  * bf16 parts hi + mid + lo = x along K (each the top 16 bits of what the one before leaves: 24 significant bits
  * in three parts of 8, none rounded; all normal for |x| ≥ 2^-103), so every product with a code is exact and
- * the sums are fp32: three times the MFMA work of the rounded route. K a multiple of 64.
+ * the sums are fp32: three times the MFMA work of the rounded route. Any K (the parts padded with zeros to
+ * whole 64-wide steps, the weight packed with zero codes past K).
  *   `group` ≠ 0: convrot, A rotated by groups of `group` in fp32 first (TensorGEMM.swift:334-345), as
  *   sq8_linear_rotated; 0: none.
  *   `scale_layout` SQ8_SCALE_COLUMNS / SQ8_SCALE_TENSOR: fp32 scales (`scale_dtype` SQ8_F32, `block` 0),
@@ -378,7 +379,8 @@ int sq8_gated_residual(sq8_ctx *ctx, float *x, int64_t ldx, const void *y, int y
  * consecutive K of an output; Sources/Siliconed/Forge/GGUF.swift, `deinterleaveQ8_0`) ---- */
 
 /* **The product on block scales**: C[m, n_out] = act(A · W + b), W[k, c] = q[k, c] · s[k / block, c],
- * int8 codes q, `block` a multiple of 32 dividing k (Q8_0: 32), k a multiple of 64. Codes in
+ * int8 codes q, `block` a multiple of 32 dividing k (Q8_0: 32), any k (A padded with zeros to whole 64-wide
+ * steps against the packed copy's zero codes). Codes in
  * `w_layout` SQ8_KN ([k, n], scales [k/block, n] row-major with the codes' row stride `ldw` — the
  * map's `[K/b, N]`; n < ldw computes the first n columns, `submit(…columns:)`) or SQ8_NK
  * ([n, k], scales [n, k/block] — GGUF's rows of blocks), scales of `scale_dtype` SQ8_F32, SQ8_BF16

@@ -352,7 +352,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
     }
     if (is_packed(wl_run) || (q.w_layout == SQ8_NK && p.a_vec && p.w_vec && k_steps && cols_per_half >= 1)) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
-        if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // packed weights need K a multiple of 64
+        if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // K = 0, or an activation not 16-byte aligned
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
         const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue), ctx->cus);
         if ((tile == sq8::WD_SKINNY32 || tile == sq8::WD_SKINNY64) && ctx->splits > 1) {
