@@ -83,7 +83,8 @@ typedef struct sq8_ctx sq8_ctx;
 /* Creates a context on HIP device `device`, launching on `stream` (a hipStream_t; NULL = the
  * device's null stream). Refuses (SQ8_ENODEVICE) a device that is not gfx950.
  * Three measurement knobs are read from the environment here, once per context: SQ8_TILE ("256",
- * "224", "128", "64", "32", "64n", "64x192", "s64", "s32": the weight-direct kernels' tile),
+ * "224", "128", "64", "32", "64n", "64x192", "s64", "s32", "gemv", "k32x32", "k32x64", "k64x64", "k64x128",
+ * "k64x192": the weight-direct kernels' tile),
  * SQ8_Q8_TILE ("256", "512", "128x256", "128x128": the block-scale kernel's tile) and SQ8_SPLITS (a
  * count ≥ 1: the skinny
  * kernel's K split over workgroups, added by a second launch; 1, the default, none; at most the

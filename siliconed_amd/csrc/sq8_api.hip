@@ -354,7 +354,7 @@ int run_product(sq8_ctx *ctx, const Product &q, double *gpu_seconds) {
         // The weight-direct kernels: packed codes, or [N, K] rows read as they lie.
         if (!p.a_vec || !k_steps) return SQ8_EUNSUPPORTED;  // K = 0, or an activation not 16-byte aligned
         const int wl = is_packed(wl_run) ? sq8::W_PACKED : sq8::W_NK;
-        const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue), ctx->cus);
+        const int tile = ctx->wd_tile >= 0 ? ctx->wd_tile : sq8::choose_wd_tile(q.m, q.n, is_glu(q.epilogue), ctx->cus, p.kt);
         if ((tile == sq8::WD_SKINNY32 || tile == sq8::WD_SKINNY64) && ctx->splits > 1) {
             // Short M with the SQ8_SPLITS knob: the K steps split over several workgroups per tile, partial
             // sums in the context's buffer, added in split order by a second launch. Not the default: the
@@ -779,7 +779,8 @@ int sq8_create(int device, void *stream, sq8_ctx **out) {
     ctx->cus = prop.multiProcessorCount;
     ctx->wd_tile = knob(getenv("SQ8_TILE"), {{"256", sq8::WD_256}, {"224", sq8::WD_224}, {"128", sq8::WD_128}, {"64", sq8::WD_64},
                                              {"32", sq8::WD_32}, {"64n", sq8::WD_64N}, {"64x192", sq8::WD_64x192}, {"s64", sq8::WD_SKINNY64}, {"s32", sq8::WD_SKINNY32},
-                                             {"gemv", sq8::WD_GEMV}});
+                                             {"gemv", sq8::WD_GEMV}, {"k32x32", sq8::WD_K32x32}, {"k32x64", sq8::WD_K32x64},
+                                             {"k64x64", sq8::WD_K64x64}, {"k64x128", sq8::WD_K64x128}, {"k64x192", sq8::WD_K64x192}});
     ctx->q8_tile = knob(getenv("SQ8_Q8_TILE"), {{"256", sq8::BL_64x256}, {"512", sq8::BL_64x512},
                                                 {"128x256", sq8::BL_128x256}, {"128x128", sq8::BL_128x128}});
     const char *splits = getenv("SQ8_SPLITS");

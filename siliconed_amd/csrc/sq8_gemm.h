@@ -53,14 +53,17 @@ hipError_t launch_gemm(const GemmArgs &p, bool fast, int tile, int wt, int wl, i
 // two per CU), WD_64N (64 × 128, a 32-column block a wave, two per CU; not GLU), WD_64x192 (64 × 192, six
 // waves of one 32-column block; not GLU), or the skinny-M kernel with 64- or 32-row tiles of one 64-column
 // slab and the K steps split over four waves (WD_SKINNY64, WD_SKINNY32), or M ≤ 64 in 16-column groups on
-// 16 × 16 MFMAs, every K step's loads issued far ahead (WD_GEMV).
+// 16 × 16 MFMAs, every K step's loads issued far ahead (WD_GEMV), or tiles of one-block waves whose K steps
+// split over two or four wave groups (WD_K32x32, WD_K32x64, WD_K64x64: four groups; WD_K64x128, WD_K64x192:
+// two; not GLU, K/64 a multiple of the groups).
 enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 4, WD_32 = 5, WD_224 = 6, WD_64N = 7, WD_64x192 = 8,
-              WD_GEMV = 9 };
+              WD_GEMV = 9, WD_K32x32 = 10, WD_K32x64 = 11, WD_K64x64 = 12, WD_K64x128 = 13, WD_K64x192 = 14 };
 // The tile for an M × N product (GLU: N = 2h): 256 or 224 rows × 256 while those tiles occupy more than
 // half the 256 CUs (the height whose rounds of 256 tiles cover the fewest rows; launch_wdirect takes
 // 128-row tiles where that kernel cannot serve the product), else the tallest of 128, 64 and 32 rows
-// whose tiles number at least 144 (enough to occupy the 256 CUs), else the skinny kernel.
-int choose_wd_tile(int M, int N, bool glu, int cus);
+// whose tiles number at least 144 (enough to occupy the 256 CUs), else the skinny kernel; below the 128-row
+// tiles, from 17 rows, the K-group tiles where one fits a round. `kt`: the product's K steps of 64.
+int choose_wd_tile(int M, int N, bool glu, int cus, int kt);
 // Bytes of the partial sums of a split skinny product (tile height bm, `splits` splits).
 int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits);
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);

@@ -19,7 +19,8 @@ hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, 
     return wl == W_NK ? launch_wdirect_1_1(p, tile, epi, out, stream) : launch_wdirect_1_2(p, tile, epi, out, stream);
 }
 
-int choose_wd_tile(int M, int N, bool glu, int cus) {
+// The tile before the K-group tiles are considered.
+static int base_wd_tile(int M, int N, bool glu, int cus) {
     // Tiles of 256 columns (four 64-column slabs; GLU: 32 output columns a slab), as tall as keeps
     // at least 9/16 of the CUs' worth of them (144 on the 256 CUs of a whole MI355X) — the measured point
     // below which a shorter tile fills the CUs better than the taller one loses (K = 3072: M = 1024 at
@@ -72,6 +73,35 @@ int choose_wd_tile(int M, int N, bool glu, int cus) {
     const long gemv_groups = glu ? (N / 2 + 7) / 8 : (N + 15) / 16;
     if (M <= 16 && gemv_groups <= cus) return WD_GEMV;
     return M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
+}
+
+int choose_wd_tile(int M, int N, bool glu, int cus, int kt) {
+    if (cus <= 0) cus = 256;
+    const int base = base_wd_tile(M, N, glu, cus);
+    // Below the 128-row tiles, from 17 rows and not for the GLU epilogues: tiles of one-block waves whose K
+    // steps split over wave groups (each group its own activation stages; the CU holds two or four times
+    // the waves and the loads in flight of the same tile). The largest of them whose tiles number between
+    // 3/4 of the CUs and the CUs, else the one with the most tiles within one round. Measured against the
+    // kernel taken without them (one process, medians of 140 launches, HIP events), M × N at K = 3072:
+    // 64 × 3072 9.6 against 13.2 µs (32 × 32, four groups), 128 × 3072 11.4 against 13.6 (32 × 64), 256 ×
+    // 3072 14.7 against 19.3 (64 × 64), C2's text stream 512 × 3072 18.6 against 20.0 (64 × 128, two
+    // groups), C0 1024 × 3072 26.3 against 28.3 (64 × 192), 64 × 9216 14.4 against 20.8, 256 × 12288 26.3
+    // against 28.2; at K = 12288, N = 3072: M = 64 19.4 against 33.8, M = 256 36.2 against 56.8.
+    if (glu || M <= 16 || base == WD_256 || base == WD_224 || base == WD_128) return base;
+    struct Cand { int tile, bm, bn, groups; };
+    static const Cand cands[] = {{WD_K64x192, 64, 192, 2}, {WD_K64x128, 64, 128, 2}, {WD_K64x64, 64, 64, 4},
+                                 {WD_K32x64, 32, 64, 4}, {WD_K32x32, 32, 32, 4}};
+    auto count = [&](const Cand &c) { return (long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
+    for (const Cand &c : cands)
+        if (kt % c.groups == 0 && count(c) >= (long)cus * 3 / 4 && count(c) <= cus) return c.tile;
+    int best = base;
+    long most = 0;
+    for (const Cand &c : cands)
+        if (kt % c.groups == 0 && count(c) <= cus && count(c) > most) {
+            best = c.tile;
+            most = count(c);
+        }
+    return best;
 }
 
 int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits) {

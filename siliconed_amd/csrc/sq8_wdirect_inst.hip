@@ -24,6 +24,34 @@ hipError_t SQ8_CAT(launch_wdirect_, SQ8_CAT(SQ8_WT, SQ8_CAT(_, SQ8_WL)))(const G
         tile = WD_128;
     }
     if (tile == WD_128) return wd::dispatch_wd<128, 4, 2, SQ8_WT, SQ8_WL>(p, epi, out, stream);
+    if (tile >= WD_K32x32 && tile <= WD_K64x192) {
+        // One-block waves whose K steps split over four or two wave groups (three activation stages a
+        // group); not for the GLU epilogues, and K/64 a multiple of the groups — else the tile of the same
+        // height without groups.
+        const bool plain = p.glu_half == 0;
+        switch (tile) {
+        case WD_K32x32:
+            if (plain && p.kt % 4 == 0) return wd::dispatch_wd<32, 1, 2, SQ8_WT, SQ8_WL, 3, 1, 4>(p, epi, out, stream);
+            tile = WD_32;
+            break;
+        case WD_K32x64:
+            if (plain && p.kt % 4 == 0) return wd::dispatch_wd<32, 2, 2, SQ8_WT, SQ8_WL, 3, 1, 4>(p, epi, out, stream);
+            tile = WD_32;
+            break;
+        case WD_K64x64:
+            if (plain && p.kt % 4 == 0) return wd::dispatch_wd<64, 2, 2, SQ8_WT, SQ8_WL, 3, 1, 4>(p, epi, out, stream);
+            tile = WD_64N;
+            break;
+        case WD_K64x128:
+            if (plain && p.kt % 2 == 0) return wd::dispatch_wd<64, 4, 2, SQ8_WT, SQ8_WL, 3, 1, 2>(p, epi, out, stream);
+            tile = WD_64N;
+            break;
+        default:
+            if (plain && p.kt % 2 == 0) return wd::dispatch_wd<64, 6, 2, SQ8_WT, SQ8_WL, 3, 1, 2>(p, epi, out, stream);
+            tile = WD_64x192;
+            break;
+        }
+    }
     if (tile == WD_64x192) {
         // Six waves of one 32-column block each: not for the GLU epilogues.
         // Four activation stages and weight buffers (C0: 28.8 against 29.1 µs with two).

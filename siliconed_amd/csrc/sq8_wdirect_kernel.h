@@ -417,8 +417,15 @@ inline bool slab_epilogue_fits(const GemmArgs &p, int epi, int out) {
 // CB: 32-column blocks a wave owns — 2 (a 64-column slab, tiles BM × 64·NW) or 1 (wave w: block w & 1 of
 // slab w ÷ 2, tiles BM × 32·NW; no GLU, no slab epilogue, two workgroups a CU): half the codes a wave widens
 // per MFMA.
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2>
-__global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(OCC, OCC)))
+// KS (one-block waves only): groups of NW waves that split the K steps — group g takes steps g, g + KS, …
+// with its own activation stages, so a CU holds KS times the waves and loads in flight for the same tile;
+// at the end the groups' sums meet in LDS and are added in group order (deterministic), then group 0 runs
+// the epilogue. K/64 must be a multiple of KS.
+constexpr int wd_waves_per_eu(int occ, int nw, int ks) { return ks == 1 ? occ : ((nw * ks + 3) / 4 > occ ? (nw * ks + 3) / 4 : occ); }
+
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2, int KS = 1>
+__global__ void __attribute__((amdgpu_flat_work_group_size(64 * NW * KS, 64 * NW * KS),
+                               amdgpu_waves_per_eu(wd_waves_per_eu(OCC, NW, KS), wd_waves_per_eu(OCC, NW, KS))))
 gemm_wd_kernel(const GemmArgs p) {
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     constexpr int FM = BM / 32;                      // 32-row blocks per wave
@@ -441,19 +448,28 @@ gemm_wd_kernel(const GemmArgs p) {
     constexpr int STEP_WAIT = WLD + (NAS - 2) * (A_PER_WAVE + WLD);
     static_assert(STEP_WAIT < 64, "vmcnt budget");
     // The slab epilogue stages the wave's whole BM × 64 bf16 outputs.
-    constexpr int LDS_BYTES = LEAN && NW * BM * 128 > LDS_STAGES ? NW * BM * 128 : LDS_STAGES;
+    constexpr int LDS_ONE = LEAN && NW * BM * 128 > LDS_STAGES ? NW * BM * 128 : LDS_STAGES;
     static_assert(!LEAN || (OUT == OUT_BF16 && (EPI == EPI_NONE || EPI == EPI_GELU)), "slab epilogue: bf16, plain or GELU");
+    static_assert(KS == 1 || (CB == 1 && OCC == 2 && !LEAN), "K groups: one-block waves");
+    // K groups: each group's stages side by side; the later groups' sums go past the epilogue regions.
+    constexpr int RED_BYTES = (KS - 1) * NW * CB * FM * 16 * 64 * 4;
+    constexpr int LDS_KS = KS * NAS * SA > NW * REGION + RED_BYTES ? KS * NAS * SA : NW * REGION + RED_BYTES;
+    constexpr int LDS_BYTES = KS == 1 || LDS_ONE > LDS_KS ? LDS_ONE : LDS_KS;
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = KS == 1 ? 0 : wave_all / NW;      // K group
+    const int wave = KS == 1 ? wave_all : wave_all - grp * NW;
+    uint8_t *const ldg = lds + grp * (NAS * SA);      // the group's activation stages
     int tm, tn;
     kern::tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM;
-    // The wave's weight columns: slab `slab`, blocks [b0, b0 + CB).
-    const int slab = CB == 2 ? tn * NW + wave : tn * (NW / 2) + (wave >> 1);
-    const int b0 = CB == 2 ? 0 : (wave & 1);
+    // The wave's weight columns: slab `slab`, blocks [b0, b0 + CB) (one-block waves: the tile's 32-column
+    // block tn·NW + wave).
+    const int slab = CB == 2 ? tn * NW + wave : (tn * NW + wave) >> 1;
+    const int b0 = CB == 2 ? 0 : ((tn * NW + wave) & 1);
     const kern::gbytes Ag = (kern::gbytes)p.a;
     const kern::gbytes Wg = (kern::gbytes)p.w;
     const int KT = p.kt;
@@ -471,12 +487,13 @@ gemm_wd_kernel(const GemmArgs p) {
         const int row = min(m0 + r, p.M - 1);
         a_goff[i] = (uint32_t)((int64_t)row * p.lda * 2) + lc * 16;
     }
+    // t: the group's own step count; its K step is t·KS + grp.
     auto issue_a = [&](int t, auto stage) {
         constexpr int S = decltype(stage)::value;
-        const kern::gbytes base = Ag + (uint32_t)min(t, KT - 1) * (BK * 2);
+        const kern::gbytes base = Ag + (uint32_t)min(t * KS + grp, KT - 1) * (BK * 2);
 #pragma unroll
         for (int i = 0; i < A_PER_WAVE; ++i)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(lds + S * SA + a_blk[i] * 1024), 16, 0,
+            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(ldg + S * SA + a_blk[i] * 1024), 16, 0,
                                              0);
     };
 
@@ -488,7 +505,7 @@ gemm_wd_kernel(const GemmArgs p) {
     u32x4 raw[NAS][WLD];
     auto issue_w = [&](int t, auto buf) {
         constexpr int B = decltype(buf)::value;
-        const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t, KT - 1)) * w_step;
+        const kern::gbytes base = Wg + (uint32_t)weight_step(p, min(t * KS + grp, KT - 1)) * w_step;
 #pragma unroll
         for (int j = 0; j < WLD; ++j) raw[B][j] = kern::gld<u32x4>(base, w_off[j]);
     };
@@ -602,7 +619,7 @@ gemm_wd_kernel(const GemmArgs p) {
             constexpr int ks = decltype(kc)::value;
             static_for<0, FM>([&](auto bmc) {
                 constexpr int bm = decltype(bmc)::value;
-                xf[ks & 1][bm] = kern::lds_load_frag(lds + S * SA + 32 * 128 * bm, xo[bm & 1][ks]);
+                xf[ks & 1][bm] = kern::lds_load_frag(ldg + S * SA + 32 * 128 * bm, xo[bm & 1][ks]);
             });
         };
         __builtin_amdgcn_sched_barrier(0);
@@ -662,20 +679,21 @@ gemm_wd_kernel(const GemmArgs p) {
             step_barrier();
         }
     };
+    const int KTG = KT / KS;  // the group's steps
     if constexpr (NAS == 2) {
         int t = 0;
-        for (; t + 1 < KT; t += 2) {
+        for (; t + 1 < KTG; t += 2) {
             one_step(t, I0{});
             one_step(t + 1, I1{});
         }
-        if (t < KT) one_step(t, I0{});
+        if (t < KTG) one_step(t, I0{});
     } else {
         // Step t + u on stage and buffer u.
         int t = 0;
-        for (; t + NAS <= KT; t += NAS)
+        for (; t + NAS <= KTG; t += NAS)
             static_for<0, NAS>([&](auto uc) { step_jit(t + decltype(uc)::value, uc, uc); });
         static_for<0, NAS - 1>([&](auto uc) {
-            if (t + decltype(uc)::value < KT) step_jit(t + decltype(uc)::value, uc, uc);
+            if (t + decltype(uc)::value < KTG) step_jit(t + decltype(uc)::value, uc, uc);
         });
     }
     // The scales and biases of the wave's columns, loaded once for all its row blocks; their latency
@@ -694,6 +712,33 @@ gemm_wd_kernel(const GemmArgs p) {
     // region over the stages.
     wait_vmcnt<0>();
     step_barrier();
+    if constexpr (KS > 1) {
+        // Groups 1 … KS−1 leave their sums in LDS ([group][wave][block][register][lane]); group 0 adds
+        // them in group order.
+        constexpr int PER_WAVE = CB * FM * 16 * 64;
+        float *red = reinterpret_cast<float *>(lds + NW * REGION);
+        if (grp > 0) {
+            float *dst = red + ((grp - 1) * NW + wave) * PER_WAVE + lane;
+#pragma unroll
+            for (int b = 0; b < CB; ++b)
+#pragma unroll
+                for (int bm = 0; bm < FM; ++bm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[((b * FM + bm) * 16 + r) * 64] = acc[b][bm][r];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < KS; ++g) {
+            const float *src = red + ((g - 1) * NW + wave) * PER_WAVE + lane;
+#pragma unroll
+            for (int b = 0; b < CB; ++b)
+#pragma unroll
+                for (int bm = 0; bm < FM; ++bm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[b][bm][r] += src[((b * FM + bm) * 16 + r) * 64];
+        }
+    }
 
     // ---- epilogue ------------------------------------------------------------------------------
     // Lane l, register r of block (b, bm): row m0 + 32·bm + (l & 31), slab column
@@ -718,8 +763,9 @@ gemm_wd_kernel(const GemmArgs p) {
     });
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2>
+template <int BM, int NW, int OCC, int WT, int WL, int EPI, int OUT, bool LEAN = false, int NAS = 2, int CB = 2, int KS = 1>
 hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
+    if (KS > 1 && args.kt % KS != 0) return hipErrorInvalidValue;
     constexpr bool GLU = EPI == EPI_SILU_GLU || EPI == EPI_SITU_GLU;
     GemmArgs p = args;
     p.tiles_m = (p.M + BM - 1) / BM;
@@ -727,19 +773,19 @@ hipError_t launch_wd(const GemmArgs &args, hipStream_t stream) {
     p.tiles_n = CB == 2 ? (slabs + NW - 1) / NW : (p.N + 32 * NW - 1) / (32 * NW);
     const int blocks = p.tiles_m * p.tiles_n;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN, NAS, CB>), dim3(blocks), dim3(64 * NW), 0, stream,
-                       p);
+    hipLaunchKernelGGL((gemm_wd_kernel<BM, NW, OCC, WT, WL, EPI, OUT, LEAN, NAS, CB, KS>), dim3(blocks), dim3(64 * NW * KS), 0,
+                       stream, p);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int OCC, int WT, int WL, int NAS = 2, int CB = 2>
+template <int BM, int NW, int OCC, int WT, int WL, int NAS = 2, int CB = 2, int KS = 1>
 hipError_t dispatch_wd(const GemmArgs &p, int epi, int out, hipStream_t stream) {
     if (CB == 1 && (epi == EPI_SILU_GLU || epi == EPI_SITU_GLU)) return hipErrorInvalidValue;
     if (CB == 2 && slab_epilogue_fits(p, epi, out))
         return epi == EPI_GELU ? launch_wd<BM, NW, OCC, WT, WL, EPI_GELU, OUT_BF16, true, NAS>(p, stream)
                                : launch_wd<BM, NW, OCC, WT, WL, EPI_NONE, OUT_BF16, true, NAS>(p, stream);
 #define SQ8_CASE(E, O)                                                                            \
-    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O, false, NAS, CB>(p, stream);
+    if (epi == E && out == O) return launch_wd<BM, NW, OCC, WT, WL, E, O, false, NAS, CB, KS>(p, stream);
     SQ8_CASE(EPI_NONE, OUT_BF16)
     SQ8_CASE(EPI_NONE, OUT_F32)
     SQ8_CASE(EPI_GELU, OUT_BF16)

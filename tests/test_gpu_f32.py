@@ -74,7 +74,8 @@ def test_rounded_route_misses_the_fp32_bar(gemm, orc):
 
 
 KERNEL_KNOBS = {"main256": "256", "main224": "224", "main128": "128", "main64": "64", "main32": "32", "main64n": "64n",
-                "main64x192": "64x192", "skinny64": "s64", "skinny32": "s32"}
+                "main64x192": "64x192", "skinny64": "s64", "skinny32": "s32", "k32x32": "k32x32", "k64x64": "k64x64",
+                "k64x192": "k64x192"}
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 64), (33, 320, 200), (130, 3072, 520), (300, 1024, 1000)],

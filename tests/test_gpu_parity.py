@@ -400,7 +400,10 @@ def test_packed_baseline_shapes(gemm, orc, case):
 # ---- every weight-direct kernel on the same problems ----------------------------------------------
 
 TILES = {"main128": "128", "main256": "256", "main224": "224", "main64n": "64n", "main64x192": "64x192",
-         "skinny64": "s64", "skinny32": "s32"}
+         "skinny64": "s64", "skinny32": "s32", "k32x32": "k32x32", "k32x64": "k32x64", "k64x64": "k64x64",
+         "k64x128": "k64x128", "k64x192": "k64x192"}
+# The K-group tiles: groups of waves that split the K steps (their sums added in group order).
+K_GROUPS = {"k32x32": 4, "k32x64": 4, "k64x64": 4, "k64x128": 2, "k64x192": 2}
 KERNEL_SHAPES = [
     (1, 64, 64),       # one K step: three of the skinny kernel's four waves have none
     (33, 320, 200),    # 5 K steps (not a multiple of the 4 waves), ragged M and N
@@ -431,6 +434,16 @@ def test_each_kernel_on_the_same_problem(gemm, orc, tile_gemm, shape, fp8):
         assert torch.equal(results[("main224", out)], results[("main128", out)])
         assert torch.equal(results[("main64n", out)], results[("main128", out)])
         assert torch.equal(results[("main64x192", out)], results[("main128", out)])
+        # The K-group tiles: one family per group count (each group's MFMA sequence, then the groups in
+        # order) where K/64 divides among the groups; else they fall back to the tiles without groups.
+        for name, groups in K_GROUPS.items():
+            if (k // 64) % groups:
+                assert torch.equal(results[(name, out)], results[("main128", out)]), name
+        if (k // 64) % 4 == 0:
+            assert torch.equal(results[("k32x64", out)], results[("k32x32", out)])
+            assert torch.equal(results[("k64x64", out)], results[("k32x32", out)])
+        if (k // 64) % 2 == 0:
+            assert torch.equal(results[("k64x192", out)], results[("k64x128", out)])
 
 
 @pytest.mark.parametrize("epi", ["silu", "situ"])
@@ -573,6 +586,36 @@ def test_one_block_waves_qkv_and_residual(gemm, orc, tile_gemm, head_dim):
         torch.cuda.synchronize()
         res[tile] = got.cpu().numpy()
     assert bitwise_equal(res["64n"], res["128"]) == 0 and bitwise_equal(res["64x192"], res["128"]) == 0
+
+
+@pytest.mark.parametrize("tile", ["k32x32", "k64x128"])
+@pytest.mark.parametrize("head_dim", [0, 64])
+def test_k_group_tiles_qkv_and_residual(gemm, orc, tile_gemm, tile, head_dim):
+    """The K-group tiles (the K steps split over four or two wave groups, the groups' sums added in order)
+    on the fused QKV split, row-major and head-major: each output the same bits as the same tile's whole
+    product; on the gated residual epilogue: the same bits as the tile's fp32 product followed by the
+    residual pass; both judged against the truth."""
+    m, k, d = 200, 1024, 192
+    x, q, s, b = problem(orc, m, k, 3 * d, False, 48 + head_dim)
+    g = tile_gemm(tile)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    whole = g.product(bf16_dev(x), w, dev(s), bias=dev(b))
+    parts = g.product_qkv(bf16_dev(x), w, dev(s), bias=dev(b), head_dim=head_dim)
+    torch.cuda.synchronize()
+    got = np.concatenate([(t.permute(1, 0, 2).reshape(m, d) if head_dim else t).float().cpu().numpy()
+                          for t in parts], axis=1)
+    assert bitwise_equal(got, whole.float().cpu().numpy()) == 0
+    judge(orc, got, x, q, False, s, b, "none", torch.bfloat16, rows=orc.sample_rows(m, 64))
+    stream = orc.normal_f32(49, (m, 3 * d), 0.0, 1.0)
+    gate = dev(orc.normal_f32(50, (3 * d,), 0.0, 0.5))
+    y = g.product(bf16_dev(x), w, dev(s), bias=dev(b), out_dtype=torch.float32)
+    expect = dev(stream)
+    g.gated_residual(expect, y, gate)
+    res = dev(stream)
+    g.product_residual(res, bf16_dev(x), w, dev(s), bias=dev(b), gate=gate)
+    torch.cuda.synchronize()
+    assert bitwise_equal(res.cpu().numpy(), expect.cpu().numpy()) == 0
+    judge(orc, y.cpu().numpy(), x, q, False, s, b, "none", torch.float32)
 
 
 def test_streams_switched_between_products(gemm, orc):

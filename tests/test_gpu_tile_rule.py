@@ -3,8 +3,9 @@
 Every tile of the weight-direct main kernels (256- and 224-row tiles, 128/64/32-row tiles of 64-column
 waves, 64 × 128 and 64 × 192 tiles of one-block waves) runs one MFMA sequence over K, so whatever the
 rule picks among them gives the bits of the 128-row tiles; the skinny kernel splits K over its waves and
-gives the bits of its own 32-row tiles, the short-M kernel (up to 16 rows) its own. So the default product
-equals one of those three bit for bit, and
+gives the bits of its own 32-row tiles, the short-M kernel (up to 16 rows) its own, and the K-group tiles
+(the K steps split over four or two wave groups) one set of bits per group count. So the default product
+equals one of those five bit for bit, and
 is judged against the oracle's fp64 truth on sampled rows at the reference's bars (Diagnostic.swift:105-107,
 DiagnosticProbes.swift:75-82).
 """
@@ -46,10 +47,11 @@ def test_default_tile_matches_a_fixed_tile(gemm, orc, tile_gemm, i):
     if layout == "packed":
         w = gemm.pack(w, layout="nk", glu=epi == "silu")
     ys = {}
-    for name, g in (("default", gemm), ("128", tile_gemm("128")), ("s32", tile_gemm("s32")), ("gemv", tile_gemm("gemv"))):
+    for name, g in (("default", gemm), ("128", tile_gemm("128")), ("s32", tile_gemm("s32")), ("gemv", tile_gemm("gemv")),
+                    ("k32x32", tile_gemm("k32x32")), ("k64x128", tile_gemm("k64x128"))):
         y = g.product(bf16_dev(x), w, dev(s), layout="nk", bias=dev(b), epilogue=_NAMES[epi], out_dtype=out)
         torch.cuda.synchronize()
         ys[name] = y.float().cpu().numpy()
-    assert any(bitwise_equal(ys["default"], ys[t]) == 0 for t in ("128", "s32", "gemv"))
+    assert any(bitwise_equal(ys["default"], ys[t]) == 0 for t in ("128", "s32", "gemv", "k32x32", "k64x128"))
     if m >= 31:
         judge(orc, ys["default"], x, q, fp8, s, b, epi, out, rows=orc.sample_rows(m, 32))
