@@ -658,7 +658,8 @@ gemm_wd_kernel(const GemmArgs p) {
         });
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<STEP_WAIT>();
-        step_barrier();
+        // Groups of one wave share no LDS within the K loop (each reads only the stages it loads itself).
+        if constexpr (NW > 1 || KS == 1) step_barrier();
     };
 
     // One step t of parity P: stage P, W(t) in raw[P]. OCC = 1 widened W(t) during step t−1 and
