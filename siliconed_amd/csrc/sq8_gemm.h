@@ -62,8 +62,17 @@ enum WdTile { WD_256 = 0, WD_128 = 1, WD_SKINNY64 = 2, WD_SKINNY32 = 3, WD_64 = 
 // half the 256 CUs (the height whose rounds of 256 tiles cover the fewest rows; launch_wdirect takes
 // 128-row tiles where that kernel cannot serve the product), else the tallest of 128, 64 and 32 rows
 // whose tiles number at least 144 (enough to occupy the 256 CUs), else the skinny kernel; below the 128-row
-// tiles, from 17 rows, the K-group tiles where one fits a round. `kt`: the product's K steps of 64.
+// tiles the K-group tiles where one fits a round (up to 16 rows only where the short-M kernel would read the
+// activation from global memory). `kt`: the product's K steps of 64.
 int choose_wd_tile(int M, int N, bool glu, int cus, int kt);
+// The short-M kernel (sq8_gemv_kernel.h): the activation staged in LDS (M rows of K' = kt · 64 bf16, rows
+// gemv_xpitch bytes apart: 16 more than a row, so the 16 rows a fragment read touches start on different banks)
+// when it fits GEMV_XLDS bytes and each row is whole 1 KB runs (K' a multiple of 512), the unit of a direct load.
+constexpr int GEMV_XLDS = 100 * 1024;
+__host__ __device__ constexpr int64_t gemv_xpitch(int kt) { return (int64_t)kt * 128 + 16; }
+__host__ __device__ constexpr bool gemv_x_in_lds(int m, int kt) {
+    return kt % 8 == 0 && (int64_t)m * gemv_xpitch(kt) <= GEMV_XLDS;
+}
 // Bytes of the partial sums of a split skinny product (tile height bm, `splits` splits).
 int64_t skinny_part_bytes(int M, int N, bool glu, int bm, int splits);
 hipError_t launch_wdirect(const GemmArgs &p, int tile, int wt, int wl, int epi, int out, hipStream_t stream);

@@ -78,7 +78,7 @@ static int base_wd_tile(int M, int N, bool glu, int cus) {
 int choose_wd_tile(int M, int N, bool glu, int cus, int kt) {
     if (cus <= 0) cus = 256;
     const int base = base_wd_tile(M, N, glu, cus);
-    // Below the 128-row tiles, from 17 rows and not for the GLU epilogues: tiles of one-block waves whose K
+    // Below the 128-row tiles and not for the GLU epilogues: tiles of one-block waves whose K
     // steps split over wave groups (each group its own activation stages; the CU holds two or four times
     // the waves and the loads in flight of the same tile). The largest of them whose tiles number between
     // 3/4 of the CUs and the CUs, else the one with the most tiles within one round. Measured against the
@@ -87,7 +87,12 @@ int choose_wd_tile(int M, int N, bool glu, int cus, int kt) {
     // 3072 14.7 against 19.3 (64 × 64), C2's text stream 512 × 3072 18.6 against 20.0 (64 × 128, two
     // groups), C0 1024 × 3072 26.3 against 28.3 (64 × 192), 64 × 9216 14.4 against 20.8, 256 × 12288 26.3
     // against 28.2; at K = 12288, N = 3072: M = 64 19.4 against 33.8, M = 256 36.2 against 56.8.
-    if (glu || M <= 16 || base == WD_256 || base == WD_224 || base == WD_128) return base;
+    // Up to 16 rows only where the short-M kernel would read the activation from global memory (it does not
+    // fit its LDS): 16 × 6144 × 3072 11.2 against 13.4 µs, 16 × 12288 × 3072 16.8 against 21.1 (M = 4 at K =
+    // 12288 fits: 13.6 against 16.6 for the K-group tile). Past one round of 16-column groups the skinny kernel
+    // stays (M = 16, K = 12288, N = 12288: 26.7 against 27.8).
+    if (glu || base == WD_256 || base == WD_224 || base == WD_128) return base;
+    if (M <= 16 && (base != WD_GEMV || gemv_x_in_lds(M, kt))) return base;
     struct Cand { int tile, bm, bn, groups; };
     static const Cand cands[] = {{WD_K64x192, 64, 192, 2}, {WD_K64x128, 64, 128, 2}, {WD_K64x64, 64, 64, 4},
                                  {WD_K32x64, 32, 64, 4}, {WD_K32x32, 32, 32, 4}};

@@ -27,14 +27,6 @@
 namespace sq8 {
 namespace wd {
 
-// The activation staged in LDS (M rows of K' = p.kt · 64 bf16, rows gemv_xpitch bytes apart: 16 more than
-// a row, so the 16 rows a fragment read touches start on different banks) when it fits GEMV_XLDS bytes and
-// each row is whole 1 KB runs (K' a multiple of 512), the unit of a direct load.
-constexpr int GEMV_XLDS = 100 * 1024;
-__host__ __device__ constexpr int64_t gemv_xpitch(int kt) { return (int64_t)kt * 128 + 16; }
-__host__ __device__ constexpr bool gemv_x_in_lds(int m, int kt) {
-    return kt % 8 == 0 && (int64_t)m * gemv_xpitch(kt) <= GEMV_XLDS;
-}
 
 template <int CG, int PF, int WT, int WL, int EPI, int OUT, bool XL>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 2)))

@@ -86,3 +86,23 @@ def test_gemv_residual(gemm, orc, tile_gemm):
     torch.cuda.synchronize()
     assert bitwise_equal(got.cpu().numpy(), expect.cpu().numpy()) == 0
     _bound_check(orc, y.cpu().numpy(), x, q.view(np.int8).astype(np.float32), s, b, "none", torch.float32, K)
+
+
+@pytest.mark.parametrize("m", [5, 16])
+def test_short_m_long_k_tile_choice(gemm, orc, tile_gemm, m):
+    """Up to 16 rows the product keeps the short-M kernel while its activation fits the kernel's LDS (M = 5 at
+    K = 6144) and takes a K-group tile where it would not (M = 16: 16 rows of 6144 bf16 exceed 100 KB): the
+    default product equals the forced kernel's bits, judged against the truth."""
+    k, n = 6144, 1024
+    x = orc.normal_bf16(70 + m, (m, k))
+    q = orc.uniform_i8(71 + m, (n, k)).view(np.uint8)
+    s = orc.uniform_f32(72 + m, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(73 + m, (n,), 0.0, 0.02)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    ys = {}
+    for name, g in (("default", gemm), ("gemv", tile_gemm("gemv")), ("k32x32", tile_gemm("k32x32"))):
+        y = g.product(bf16_dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        ys[name] = y.cpu().numpy()
+    assert bitwise_equal(ys["default"], ys["gemv" if m == 5 else "k32x32"]) == 0
+    _bound_check(orc, ys["default"], x, q.view(np.int8).astype(np.float32), s, b, "gelu", torch.float32, k)
