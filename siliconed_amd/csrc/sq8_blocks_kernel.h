@@ -57,6 +57,8 @@ __device__ __forceinline__ void store_block_t(const GemmArgs &p, const f32x16 &x
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
     constexpr int PITCH = 32 * ESZ + 16;
     const int h = lane >> 5, c = lane & 31;
+    wd::ResidualPre pre;
+    if constexpr (EPI == EPI_RESIDUAL) wd::load_residual(p, col0, m_first, n_out, lane, pre);
     static_for<0, 16>([&](auto rc) {
         constexpr int r = decltype(rc)::value;
         float v = __fadd_rn(x[r], bx);
@@ -72,7 +74,7 @@ __device__ __forceinline__ void store_block_t(const GemmArgs &p, const f32x16 &x
         else
             *reinterpret_cast<float *>(dst) = v;
     });
-    wd::flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
+    wd::flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane, EPI == EPI_RESIDUAL ? &pre : nullptr);
 }
 
 // NB: 32-column blocks per wave — 2 (the wave owns a 64-column slab) or 1 (waves in pairs share a

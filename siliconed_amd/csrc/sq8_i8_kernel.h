@@ -231,6 +231,8 @@ gemm_i8_kernel(const GemmArgs p) {
 
     // ---- epilogue: float(acc) · (s_x · s_w), then bias and activation (store_block) ----------------
     uint8_t *region = lds + wave * REGION;
+    ResidualPre pre[2];
+    if constexpr (EPI == EPI_RESIDUAL && !GLU) load_residual(p, slab * 64, m0, n_out, lane, pre[0]);
     static_for<0, FM>([&](auto bmc) {
         constexpr int bm = decltype(bmc)::value;
         ColParams cq[2];
@@ -251,9 +253,18 @@ gemm_i8_kernel(const GemmArgs p) {
         static_for<0, GLU ? 1 : 2>([&](auto bc) {
             constexpr int b = decltype(bc)::value;
             const int col0 = GLU ? slab * 32 : slab * 64 + 32 * b;
-            if (col0 < n_out)
+            if constexpr (EPI == EPI_RESIDUAL && !GLU) {
+                // The next block's residual operands load while this one is staged and stored.
+                constexpr int j = 2 * bm + b;
+                if constexpr (j + 1 < 2 * FM)
+                    load_residual(p, slab * 64 + 32 * ((j + 1) & 1), m0 + 32 * ((j + 1) >> 1), n_out, lane, pre[(j + 1) & 1]);
+                if (col0 < n_out)
+                    store_block<EPI, OUT>(p, xf32[b], cq[b], xf32[b], cq[b], has_bias, col0, m0 + 32 * bm, n_out, region,
+                                          lane, &pre[j & 1]);
+            } else if (col0 < n_out) {
                 store_block<EPI, OUT>(p, xf32[b], cq[b], xf32[GLU ? 1 : b], cq[GLU ? 1 : b], has_bias, col0, m0 + 32 * bm,
                                       n_out, region, lane);
+            }
         });
     });
 }

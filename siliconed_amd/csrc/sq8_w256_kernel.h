@@ -267,11 +267,23 @@ gemm_w256_kernel(const GemmArgs p) {
     } else {
         constexpr int REGION = 32 * (32 * (OUT == OUT_BF16 ? 2 : 4) + 16);
         uint8_t *region = lds + wave * REGION;
+        ResidualPre pre[2];
+        if constexpr (EPI == EPI_RESIDUAL && !GLU) load_residual(p, col0, m0, n_out, lane, pre[0]);
         static_for<0, FM>([&](auto bmc) {
             constexpr int bm = decltype(bmc)::value;
             if constexpr (GLU) {
                 store_block<EPI, OUT>(p, acc[0][bm], cp[0], acc[1][bm], cp[1], has_bias, col0, m0 + 32 * bm, n_out,
                                       region, lane);
+            } else if constexpr (EPI == EPI_RESIDUAL) {
+                // The next block's residual operands load while this one is staged and stored.
+                static_for<0, 2>([&](auto bc) {
+                    constexpr int b = decltype(bc)::value, j = 2 * bm + b;
+                    if constexpr (j + 1 < 2 * FM)
+                        load_residual(p, col0 + 32 * ((j + 1) & 1), m0 + 32 * ((j + 1) >> 1), n_out, lane, pre[(j + 1) & 1]);
+                    if (col0 + 32 * b < n_out)
+                        store_block<EPI, OUT>(p, acc[b][bm], cp[b], acc[b][bm], cp[b], has_bias, col0 + 32 * b, m0 + 32 * bm,
+                                              n_out, region, lane, &pre[j & 1]);
+                });
             } else {
                 static_for<0, 2>([&](auto bc) {
                     constexpr int b = decltype(bc)::value;

@@ -156,12 +156,35 @@ __device__ __forceinline__ void load_col_params(const GemmArgs &p, ColParams &cp
     }
 }
 
+// The residual epilogue's operands of one 32 × 32 block, loaded before the block's values are staged so
+// their memory latency overlaps the staging: the 16-byte segments of the fp32 stream this lane adds to
+// (rows lane/8 + 8i, columns col0 + 4·(lane & 7) … + 3, as flush_region stores them) and the gate of those
+// columns. Only whole, 16-byte-aligned segments inside the product (`vec`); the rest take the per-value path.
+struct ResidualPre {
+    f32x4 x[4];
+    f32x4 g;
+};
+__device__ __forceinline__ void load_residual(const GemmArgs &p, int col0, int m_first, int n_out, int lane,
+                                              ResidualPre &r) {
+    const int col = col0 + 4 * (lane & 7);
+    const bool vec = col + 4 <= n_out && p.c_vec16;
+    r.g = vec && p.gate ? *reinterpret_cast<const f32x4 *>(p.gate + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m_first + (lane >> 3) + 8 * i;
+        r.x[i] = vec && m < p.M ? *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.c[0]) +
+                                                                 (int64_t)m * p.ldc + col)
+                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 // The second half of an epilogue: a wave's LDS region of 32 rows × 32 finished values (row pitch
 // 32·size + 16) read back as 16-byte row segments and stored (the residual epilogue adds them to
-// the fp32 stream). Output columns [col0, col0 + 32), rows [m_first, m_first + 32).
+// the fp32 stream, whose segments `pre` holds when load_residual read them first). Output columns
+// [col0, col0 + 32), rows [m_first, m_first + 32).
 template <int EPI, int OUT>
 __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_first, int n_out, const uint8_t *region,
-                                             int lane) {
+                                             int lane, const ResidualPre *pre = nullptr) {
     constexpr int ESZ = OUT == OUT_BF16 ? 2 : 4;
     constexpr int PITCH = 32 * ESZ + 16;
     // 16-byte row segments: CPR chunks per row, 64/CPR rows per pass. LDS operations
@@ -197,8 +220,9 @@ __device__ __forceinline__ void flush_region(const GemmArgs &p, int col0, int m_
                 static_assert(OUT == OUT_F32, "the residual stream is fp32");
                 float *xr = reinterpret_cast<float *>(p.c[0]) + (int64_t)m * p.ldc + col;
                 if (col + PER <= n_out && p.c_vec16) {
-                    const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr);
-                    const f32x4 gv = p.gate ? *reinterpret_cast<const f32x4 *>(p.gate + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+                    const f32x4 xv = pre ? pre->x[i] : *reinterpret_cast<const f32x4 *>(xr);
+                    const f32x4 gv = pre ? pre->g
+                                         : p.gate ? *reinterpret_cast<const f32x4 *>(p.gate + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
                     f32x4 o;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) o[e] = __fadd_rn(xv[e], __fmul_rn(gv[e], __uint_as_float(v[e])));
@@ -322,16 +346,24 @@ __device__ __forceinline__ void stage_block(const f32x16 &x, const ColParams &cx
     });
 }
 
-// (The bias test is one uniform branch around the whole block, not a select per value.)
+// (The bias test is one uniform branch around the whole block, not a select per value.) The residual
+// epilogue's operands: `pre` when the caller loaded them ahead (a block earlier), else loaded here first.
 template <int EPI, int OUT>
 __device__ __forceinline__ void store_block(const GemmArgs &p, const f32x16 &x, const ColParams &cx, const f32x16 &u,
                                             const ColParams &cu, bool has_bias, int col0, int m_first, int n_out,
-                                            uint8_t *region, int lane) {
+                                            uint8_t *region, int lane, const ResidualPre *pre = nullptr) {
+    ResidualPre own;
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (!pre) {
+            load_residual(p, col0, m_first, n_out, lane, own);
+            pre = &own;
+        }
+    }
     if (has_bias)
         stage_block<EPI, OUT, true>(x, cx, u, cu, region, lane);
     else
         stage_block<EPI, OUT, false>(x, cx, u, cu, region, lane);
-    flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane);
+    flush_region<EPI, OUT>(p, col0, m_first, n_out, region, lane, EPI == EPI_RESIDUAL ? pre : nullptr);
 }
 
 // The 16 values of one accumulator block as 8 bf16 pairs (block_values, then nearest-even pairs).
