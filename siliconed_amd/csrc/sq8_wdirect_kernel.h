@@ -50,6 +50,24 @@ constexpr int BK = 64;
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef const __attribute__((address_space(1))) void *glb_ptr;
 
+// Direct loads through a buffer resource: the K step's byte offset rides in a scalar register (soffset) beside
+// each lane's constant 32-bit offset, so a load needs no per-lane 64-bit address add. The resource spans the
+// whole 32-bit offset range from `base` (raw, stride 0; the gfx9 family's word 3); every offset used here is
+// the one the global load would have added to the same base.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint32_t *lds_u32;
+__device__ void raw_buffer_load_lds(i32x4 rsrc, lds_u32 lds, int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ __forceinline__ i32x4 buffer_rsrc(const void *base) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)b);
+    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(b >> 32));
+    r[2] = -1;
+    r[3] = 0x00020000;
+    return r;
+}
+
 __device__ __forceinline__ int swz(int r, int lc) { return r * 128 + ((lc ^ ((r ^ (r >> 3)) & 7)) << 4); }
 
 // s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt at their maxima).
@@ -502,7 +520,6 @@ gemm_wd_kernel(const GemmArgs p) {
     // block tn·NW + wave).
     const int slab = CB == 2 ? tn * NW + wave : (tn * NW + wave) >> 1;
     const int b0 = CB == 2 ? 0 : ((tn * NW + wave) & 1);
-    const kern::gbytes Ag = (kern::gbytes)p.a;
     const kern::gbytes Wg = (kern::gbytes)p.w;
     const int KT = p.kt;
 
@@ -519,14 +536,15 @@ gemm_wd_kernel(const GemmArgs p) {
         const int row = min(m0 + r, p.M - 1);
         a_goff[i] = (uint32_t)((int64_t)row * p.lda * 2) + lc * 16;
     }
-    // t: the group's own step count; its K step is t·KS + grp.
+    // t: the group's own step count; its K step is t·KS + grp. Through a buffer resource: the step's offset
+    // in a scalar register, no per-lane address add.
+    const i32x4 a_rsrc = buffer_rsrc(p.a);
     auto issue_a = [&](int t, auto stage) {
         constexpr int S = decltype(stage)::value;
-        const kern::gbytes base = Ag + (uint32_t)min(t * KS + grp, KT - 1) * (BK * 2);
+        const int soff = __builtin_amdgcn_readfirstlane((int)((uint32_t)min(t * KS + grp, KT - 1) * (BK * 2)));
 #pragma unroll
         for (int i = 0; i < A_PER_WAVE; ++i)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(base + a_goff[i]), (lds_ptr)(ldg + S * SA + a_blk[i] * 1024), 16, 0,
-                                             0);
+            raw_buffer_load_lds(a_rsrc, (lds_u32)(ldg + S * SA + a_blk[i] * 1024), 16, (int)a_goff[i], soff, 0, 0);
     };
 
     // ---- weight loads: WLD × 16 bytes per lane per K step (load j: block b0 + j ÷ 2, half j & 1) ------
