@@ -70,8 +70,12 @@ static int base_wd_tile(int M, int N, bool glu, int cus) {
     // workgroup. Kernel traces at K = 3072, N = 3072 (int8 packed, bias): M = 1 4.10 µs against the skinny
     // kernel's 7.44, M = 16 5.95 against 8.73; K = 12288, N = 3072: M = 1 10.1 against 19.4. Past one round
     // (N = 9216, 12288) the skinny kernel's 64-column slabs stream better (M = 8: 8.3 against 11.6 µs).
+    // Without GLU also two groups a workgroup where one round holds them (N = 6144, M = 1: 7.4 against the
+    // skinny kernel's 9.7 µs; M = 16: 9.6 against 10.9), and three for a single row (N = 9216: 8.9 against
+    // 9.7; N = 12288: 10.6 against 11.4; at M = 16 the skinny kernel's 10.9 and 11.8 against 11.5 and 13.5).
     const long gemv_groups = glu ? (N / 2 + 7) / 8 : (N + 15) / 16;
     if (M <= 16 && gemv_groups <= cus) return WD_GEMV;
+    if (M <= 16 && !glu && (gemv_groups <= 2L * cus || (M == 1 && gemv_groups <= 3L * cus))) return WD_GEMV;
     return M <= 128 ? WD_SKINNY32 : WD_SKINNY64;
 }
 
@@ -93,6 +97,8 @@ int choose_wd_tile(int M, int N, bool glu, int cus, int kt) {
     // stays (M = 16, K = 12288, N = 12288: 26.7 against 27.8).
     if (glu || base == WD_256 || base == WD_224 || base == WD_128) return base;
     if (M <= 16 && (base != WD_GEMV || gemv_x_in_lds(M, kt))) return base;
+    // The short-M kernel's several groups a workgroup were measured with the activation in LDS only.
+    if (M <= 16 && (N + 15) / 16 > cus) return WD_SKINNY32;
     struct Cand { int tile, bm, bn, groups; };
     static const Cand cands[] = {{WD_K64x192, 64, 192, 2}, {WD_K64x128, 64, 128, 2}, {WD_K64x64, 64, 64, 4},
                                  {WD_K32x64, 32, 64, 4}, {WD_K32x32, 32, 32, 4}};

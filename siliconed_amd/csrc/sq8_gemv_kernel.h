@@ -216,14 +216,15 @@ gemm_gemv_kernel(const GemmArgs p) {
     }
 }
 
-// Column groups of 16 a workgroup: the most of 4, 2, 1 that still gives at least 3/4 of the CUs a
-// workgroup (more groups, less activation re-read per column; fewer, more CUs streaming the weight).
+// Column groups of 16 a workgroup: the fewest that fit the groups in one round of workgroups on the CUs
+// (1 … 4; more, four a workgroup in more rounds). Measured at K = 3072, M = 1 (one process, HIP events):
+// N = 6144 two groups 7.4 µs against 8.2 with one (two rounds), N = 9216 three 8.9 against 11.8 with two,
+// N = 12288 three 10.6 against 11.2 with four (192 workgroups).
 inline int gemv_groups_per_wg(const GemmArgs &p, bool glu) {
     const int groups = glu ? (p.glu_half + 7) / 8 : (p.N + 15) / 16;
     const int cus = p.cus > 0 ? p.cus : 256;
-    for (int cg = 4; cg > 1; cg /= 2)
-        if ((groups + cg - 1) / cg >= cus * 3 / 4) return cg;
-    return 1;
+    const int cg = (groups + cus - 1) / cus;
+    return cg < 1 ? 1 : cg > 4 ? 4 : cg;
 }
 
 template <int CG, int PF, int WT, int WL, int EPI, int OUT>
@@ -242,9 +243,10 @@ hipError_t launch_gemv(const GemmArgs &p, hipStream_t stream) {
     if (p.M > 16) return hipErrorInvalidValue;
     const int groups = GLU ? (p.glu_half + 7) / 8 : (p.N + 15) / 16;
     if (groups == 0 || p.M == 0) return hipSuccess;
-    // Steps of code loads in flight: eight of one group, six of two, four of four (the registers).
+    // Steps of code loads in flight: eight of one group, six of two, five of three, four of four (the registers).
     switch (gemv_groups_per_wg(p, GLU)) {
     case 4: return launch_gemv_cg<4, 4, WT, WL, EPI, OUT>(p, groups, stream);
+    case 3: return launch_gemv_cg<3, 5, WT, WL, EPI, OUT>(p, groups, stream);
     case 2: return launch_gemv_cg<2, 6, WT, WL, EPI, OUT>(p, groups, stream);
     default: return launch_gemv_cg<1, 8, WT, WL, EPI, OUT>(p, groups, stream);
     }

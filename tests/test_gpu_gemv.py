@@ -3,7 +3,7 @@ waves, every step's loads issued far ahead, the activation staged in LDS where i
 forced through the SQ8_TILE knob, on every route and epilogue it serves, judged element by element against
 the oracle's fp64 truth with the short-product bound of test_gpu_small_m (the per-channel metric is
 ill-conditioned on a handful of rows). Rows 1 … 16 (more rows take the skinny kernel under the same knob),
-column counts that give one, two and four groups a workgroup (ragged), packed and [N, K] codes, the
+column counts that give one, two, three and four groups a workgroup (ragged), packed and [N, K] codes, the
 activation in LDS (K a multiple of 512) and not."""
 import numpy as np
 import pytest
@@ -16,8 +16,9 @@ from test_gpu_small_m import _bound_check
 pytestmark = pytest.mark.gpu
 K = 3072
 
-# (epilogue, output columns): 1, 2 and 4 column groups a workgroup on 256 CUs, each count ragged.
-CASES = [("none", 200), ("gelu", 6160), ("none", 12304), ("silu", 136), ("silu", 3080), ("silu", 6152)]
+# (epilogue, output columns): 1, 2, 3 and 4 column groups a workgroup on 256 CUs, each count ragged.
+CASES = [("none", 200), ("gelu", 6160), ("none", 9232), ("none", 12304), ("silu", 136), ("silu", 3080),
+         ("silu", 4616), ("silu", 6152)]
 
 
 @pytest.mark.parametrize("m", [1, 5, 16])
