@@ -155,11 +155,11 @@ gemm_i8_kernel(const GemmArgs p) {
         static_for<0, 4>([&](auto sc) {
             constexpr int s = decltype(sc)::value;
             if constexpr (s < 3) read_x(std::integral_constant<int, s + 1>{});
-            static_for<0, 2>([&](auto bc) {
-                constexpr int b = decltype(bc)::value;
-                const i32x4 w = __builtin_bit_cast(i32x4, raw[P][4 * (s >> 1) + 2 * b + (s & 1)]);
-                static_for<0, FM>([&](auto bmc) {
-                    constexpr int bm = decltype(bmc)::value;
+            static_for<0, FM>([&](auto bmc) {  // row block outer: a fragment's MFMAs back to back
+                constexpr int bm = decltype(bmc)::value;
+                static_for<0, 2>([&](auto bc) {
+                    constexpr int b = decltype(bc)::value;
+                    const i32x4 w = __builtin_bit_cast(i32x4, raw[P][4 * (s >> 1) + 2 * b + (s & 1)]);
                     acc[b][bm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, xf[s & 1][bm], acc[b][bm], 0, 0, 0);
                 });
             });

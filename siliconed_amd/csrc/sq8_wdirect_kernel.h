@@ -616,10 +616,10 @@ gemm_wd_kernel(const GemmArgs p) {
                     wf[1 - F][b][q] = widen8<WT>(r[2 * (q & 1)], r[2 * (q & 1) + 1]);
                 });
             }
-            static_for<0, CB>([&](auto bc) {
-                constexpr int b = decltype(bc)::value;
-                static_for<0, FM>([&](auto bmc) {
-                    constexpr int bm = decltype(bmc)::value;
+            static_for<0, FM>([&](auto bmc) {  // row block outer: a fragment's MFMAs back to back
+                constexpr int bm = decltype(bmc)::value;
+                static_for<0, CB>([&](auto bc) {
+                    constexpr int b = decltype(bc)::value;
                     acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[F][b][ks], xf[ks & 1][bm], acc[b][bm], 0, 0, 0);
                 });
             });
@@ -689,10 +689,10 @@ gemm_wd_kernel(const GemmArgs p) {
                 issue_w(t + NAS, std::integral_constant<int, P>{});
                 __builtin_amdgcn_sched_barrier(0);
             }
-            static_for<0, CB>([&](auto bc) {
-                constexpr int b = decltype(bc)::value;
-                static_for<0, FM>([&](auto bmc) {
-                    constexpr int bm = decltype(bmc)::value;
+            static_for<0, FM>([&](auto bmc) {  // row block outer: a fragment's MFMAs back to back
+                constexpr int bm = decltype(bmc)::value;
+                static_for<0, CB>([&](auto bc) {
+                    constexpr int b = decltype(bc)::value;
                     acc[b][bm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wk[ks & 1][b], xf[ks & 1][bm], acc[b][bm], 0, 0, 0);
                 });
             });
