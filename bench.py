@@ -344,6 +344,9 @@ def main() -> int:
     ap.add_argument("--layout", choices=["kn", "nk", "packed"], default="packed",
                     help="weight layout the product reads; packed = staged once by sq8_pack_weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--operands", choices=["synthetic", "zero-x", "ones-x", "zero-w"], default="synthetic",
+                    help="diagnostic: the same launches on constant operands (all activations 0 or 1, or all codes 0), "
+                         "which change the power the products draw and so the clock, not the work; the line says so")
     ap.add_argument("--shape", metavar="MxKxN", default=None,
                     help="the workload's product at another M, K, N (same weight type, epilogue and inputs' "
                          "distributions); the line then carries no measured traffic")
@@ -384,6 +387,12 @@ def main() -> int:
     glu = epi == "silu_glu"
     qkv = epi == "qkv"
     x, q, s, b = inputs(args.workload)
+    if args.operands == "zero-x":
+        x = torch.zeros_like(x)
+    elif args.operands == "ones-x":
+        x = torch.ones_like(x)
+    elif args.operands == "zero-w":
+        q = np.zeros_like(q) if isinstance(q, np.ndarray) else torch.zeros_like(q)
     xd = x.to(dev)
     sd = torch.from_numpy(s).to(dev)
     bd = torch.from_numpy(b).to(dev)
@@ -545,7 +554,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8" if w8a8 else "f32" if args.workload in EXACT else "bf16",
-        "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}",
+        "data": f"synthetic, seeded (SplitMix64 + Box-Muller), seeds {SEEDS}"
+                + ("" if args.operands == "synthetic" else f"; DIAGNOSTIC operands {args.operands}"),
         "config": {"workload": f"{args.workload}: {desc}", "M": M, "K": K, "N": N, "weight_type": wt,
                    "weight_layout": args.layout.upper(),
                    "staging_ms": None if stage_ms is None else round(stage_ms, 3), "global_batch": M,
