@@ -107,3 +107,23 @@ def test_short_m_long_k_tile_choice(gemm, orc, tile_gemm, m):
         ys[name] = y.cpu().numpy()
     assert bitwise_equal(ys["default"], ys["gemv" if m == 5 else "k32x32"]) == 0
     _bound_check(orc, ys["default"], x, q.view(np.int8).astype(np.float32), s, b, "gelu", torch.float32, k)
+
+
+@pytest.mark.parametrize("m,n,kernel", [(1, 6144, "gemv"), (16, 6144, "gemv"), (1, 9216, "gemv"), (1, 12288, "gemv"),
+                                        (8, 9216, "s32"), (16, 12288, "s32")])
+def test_wide_short_m_tile_choice(gemm, orc, tile_gemm, m, n, kernel):
+    """Past one round of 16-column groups the product keeps the short-M kernel with two groups a workgroup up to
+    N = 8192, and with three for a single row up to N = 12288; more rows there take the skinny kernel. The default
+    product equals the expected kernel's bits, judged against the truth."""
+    x = orc.normal_bf16(80 + m, (m, K))
+    q = orc.uniform_i8(81 + m, (n, K)).view(np.uint8)
+    s = orc.uniform_f32(82 + m, (n,), 1e-3, 2e-2)
+    b = orc.normal_f32(83 + m, (n,), 0.0, 0.02)
+    w = gemm.pack(weight_tensor(q, False, "nk"), layout="nk")
+    ys = {}
+    for name, g in (("default", gemm), (kernel, tile_gemm(kernel))):
+        y = g.product(bf16_dev(x), w, dev(s), bias=dev(b), epilogue="gelu_tanh", out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        ys[name] = y.cpu().numpy()
+    assert bitwise_equal(ys["default"], ys[kernel]) == 0
+    _bound_check(orc, ys["default"], x, q.view(np.int8).astype(np.float32), s, b, "gelu", torch.float32, K)
