@@ -281,8 +281,10 @@ hipError_t launch_norm_modulate(const float *x, int64_t ldx, const float *w, con
     if (rows == 0 || cols == 0) return hipSuccess;
     const bool vec = cols % 4 == 0 && ldx % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 7) == 0;
     auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-    // The row held in registers (norm_operand_kernel without a rotation): x read once instead of twice,
-    // the same operations in the same order, so the same bits.
+    // norm_operand_kernel without a rotation: the same operations in the same order, so the same bits (its
+    // second pass over x finds the row in the caches). A version holding four rows a workgroup in registers,
+    // x loaded once and the vectors once per four rows, ran the C4 block's 4608 × 3072 rows in the same
+    // 21.8 µs (85 MB at 3.9 TB/s): not kept.
     if (vec && a16(w) && a16(scale) && a16(shift) && cols <= 8 * 4096)
         return launch_norm_operand(x, ldx, w, scale, shift, eps, rows, cols, 0, nullptr, 0, out, ldo, nullptr, 0, 0,
                                    nullptr, stream);
